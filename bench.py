@@ -1,0 +1,304 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline workload (metric quoted on it): GGML_OP_FLASH_ATTN_EXT decode over a
+32k-context q8_0 KV cache — n_q = 1, 24 Q heads / 4 KV heads, head_dim 256,
+KV length 32768, 4 independent sequences, all-visible F16 mask, scale 1/16. The
+gated-delta-net decode step (16 k-heads / 32 v-heads, d = 128, f32 state, 8
+sequences) is measured in the same run because the metric names both.
+
+One "step" is one call of the op on inputs already resident in HBM. Input sets
+are rotated (>= 512 MiB in total) so the 256 MB Infinity Cache cannot serve
+repeats. Reported:
+  value        whole-call algorithmic HBM GB/s of the FA decode (bytes the op
+               must move once: K + V + Q + O + mask) / event-timed µs per call;
+  roofline     the dominant kernel (fa_pass1) alone: algorithmic bytes of one
+               launch / its average device duration from HIP events recorded
+               around each launch on the library's stream; peak 8 TB/s;
+  cpu_baseline the ggml-CPU restatement (oracle/, "port") on the host cores of
+               this box, on the same workload bytes.
+Synthetic data: torch's device generator for N(0,1) K/V rows, quantised on the
+GPU by the library's bit-exact ggml q8_0 quantizer.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "xllama-qwen35-xbox_amd"))
+
+METRIC = "µs/call + achieved HBM GB/s (% of 8 TB/s) for FA decode @32k and GDN step"
+PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def make_fa_sets(torch, xq, wl, cfg, n_sets, seed=0):
+    """KV caches (q8_0 via the GPU quantizer), Q, mask and dst per input set."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    B, L, Hkv, D, H, NQ = cfg.B, cfg.L, cfg.Hkv, cfg.D, cfg.H, cfg.n_q
+    rec = wl.record_bytes(cfg.kv_type, D)
+    sets = []
+    rows_chunk = 8192
+    for s in range(n_sets):
+        planes = []
+        for _ in range(2):  # K then V
+            plane = torch.empty(B * L * Hkv * rec, dtype=torch.uint8, device="cuda")
+            for r0 in range(0, B * L, rows_chunk):
+                n = min(rows_chunk, B * L - r0)
+                x = torch.randn((n, Hkv, D), generator=gen, device="cuda", dtype=torch.float32)
+                pos = torch.arange(r0, r0 + n, device="cuda", dtype=torch.int32)
+                xq.kv_store(x, pos, Hkv, D, cfg.kv_type, plane, B * L)
+            planes.append(plane)
+        k = xq.DevTensor(cfg.kv_type, (D, L, Hkv, B), (wl.TYPE_SIZE[cfg.kv_type], Hkv * rec, rec, L * Hkv * rec), planes[0])
+        v = xq.DevTensor(cfg.kv_type, (D, L, Hkv, B), (wl.TYPE_SIZE[cfg.kv_type], Hkv * rec, rec, L * Hkv * rec), planes[1])
+        qt = torch.randn((B, NQ, H, D), generator=gen, device="cuda", dtype=torch.float32)
+        q = xq.DevTensor(wl.F32, (D, NQ, H, B), (4, H * D * 4, D * 4, NQ * H * D * 4), qt)
+        mt = torch.zeros((B, NQ, L), dtype=torch.float16, device="cuda")  # all-visible, one row per sequence
+        m = xq.DevTensor(wl.F16, (L, NQ, 1, B), (2, L * 2, NQ * L * 2, NQ * L * 2), mt)
+        dt = torch.empty((B, NQ, H, D), dtype=torch.float32, device="cuda")
+        d = xq.DevTensor(wl.F32, (D, H, NQ, B), (4, D * 4, H * D * 4, NQ * H * D * 4), dt)
+        sets.append((q, k, v, m, d))
+    torch.cuda.synchronize()
+    return sets
+
+
+def make_gdn_sets(torch, xq, wl, cfg, n_sets, seed=1):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    B, T, K = cfg.B, cfg.T, cfg.slots
+    sets = []
+    for _ in range(n_sets):
+        qf = torch.nn.functional.normalize(torch.randn((B, T, 16, 128), generator=gen, device="cuda"), dim=-1)
+        kf = torch.nn.functional.normalize(torch.randn((B, T, 16, 128), generator=gen, device="cuda"), dim=-1)
+        vf = torch.randn((B, T, 32, 128), generator=gen, device="cuda")
+        beta = torch.sigmoid(torch.randn((B, T, 32), generator=gen, device="cuda"))
+        g = -torch.nn.functional.softplus(torch.randn((B, T, 32), generator=gen, device="cuda"))
+        st = torch.randn((B, 32, 128, 128), generator=gen, device="cuda") * 0.1
+        rows = T + K * 128
+        dst = torch.empty((B, rows, 4096), dtype=torch.float32, device="cuda")
+        F = wl.F32
+        mk = lambda t, ne: xq.DevTensor(F, ne, (4, 4 * ne[0], 4 * ne[0] * ne[1], 4 * ne[0] * ne[1] * ne[2]), t)
+        sets.append((mk(qf, (128, 16, T, B)), mk(kf, (128, 16, T, B)), mk(vf, (128, 32, T, B)),
+                     mk(g, (1, 32, T, B)), mk(beta, (1, 32, T, B)), mk(st, (128, 128, 32, B)),
+                     xq.DevTensor(F, (4096, rows, B, 1), (4, 16384, 16384 * rows, 16384 * rows * B), dst)))
+    torch.cuda.synchronize()
+    return sets
+
+
+def time_calls(torch, fn, n_sets, steps, warmup):
+    for i in range(warmup):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i % n_sets)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per call
+
+
+def kernel_times(torch, xq, fn, n_sets, steps):
+    xq.profile_reset()
+    xq.profile_enable(True)
+    for i in range(steps):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    xq.profile_enable(False)
+    res = xq.profile_read()
+    xq.profile_reset()
+    return {k: {"avg_us": 1000.0 * ms / max(n, 1), "launches": n} for k, (ms, n) in res.items()}
+
+
+def cpu_fa_baseline(torch, wl, cfg, fa_set, threads, budget_s):
+    """ggml-CPU restatement on the same bytes (copied back to host)."""
+    import numpy as np
+    import oracle
+    q, k, v, m, d = fa_set
+    host = lambda dt, t: wl.HostTensor(dt.type, dt.ne, dt.nb, t.t.reshape(-1).view(torch.uint8).cpu().numpy())
+    hq, hk, hv, hm = host(q, q), host(k, k), host(v, v), host(m, m)
+    hd = wl.HostTensor(wl.F32, d.ne, d.nb, np.zeros(d.t.numel() * 4, np.uint8))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        oracle.flash_attn_ext(hq, hk, hv, hm, None, hd, cfg.kq_scale, 0.0, 0.0, oracle.QK_CONSISTENT, True,
+                              threads, want_lse=False)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 3 and time.perf_counter() > t_end:
+            break
+        if len(times) >= 20:
+            break
+    # parity spot check of the measured GPU output against the same CPU run
+    got = np.frombuffer(d.t.cpu().numpy().tobytes(), np.float32)
+    want = np.frombuffer(hd.buf.tobytes(), np.float32)
+    max_err = float(np.max(np.abs(got - want)))
+    return statistics.median(times), len(times), max_err
+
+
+def cpu_gdn_baseline(torch, wl, gdn_set, slots, threads, budget_s):
+    import numpy as np
+    import oracle
+    hs = [wl.HostTensor(t.type, t.ne, t.nb, t.t.reshape(-1).view(torch.uint8).cpu().numpy()) for t in gdn_set]
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        oracle.gated_delta_net(*hs[:6], hs[6], slots, threads)
+        times.append(time.perf_counter() - t0)
+        if (len(times) >= 3 and time.perf_counter() > t_end) or len(times) >= 50:
+            break
+    got = np.frombuffer(gdn_set[6].t.cpu().numpy().tobytes(), np.float32)
+    want = np.frombuffer(hs[6].buf.tobytes(), np.float32)
+    return statistics.median(times), len(times), float(np.max(np.abs(got - want)))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work per baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    import xqattn as xq
+    from xqattn import workloads as wl
+
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        sys.exit(1)
+    xq.load()
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device {dev.name} ({getattr(dev, 'gcnArchName', '?')}), libxqattn ABI {xq.abi_version()}")
+
+    if args.calib_copy:
+        a = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration copy of 512 MiB done")
+        del a, b
+
+    # ---------------- FA decode @32k q8_0 (headline)
+    cfg = wl.FA_C2
+    n_sets = max(2, math.ceil(512 * 2**20 / cfg.kv_bytes()))
+    log(f"building {n_sets} input sets of {cfg.name} ({cfg.kv_bytes() / 1e6:.1f} MB KV each)")
+    sets = make_fa_sets(torch, xq, wl, cfg, n_sets)
+    params = xq.fa_params(cfg.kq_scale)
+    q, k, v, m, d = sets[0]
+    ws = torch.empty(xq.flash_attn_ext_workspace(q, k, v, m, None, d, params) + 256,
+                     dtype=torch.uint8, device="cuda")
+
+    def fa_call(i):
+        q, k, v, m, d = sets[i]
+        xq.flash_attn_ext(q, k, v, m, None, d, params, workspace=ws)
+
+    log(f"FA: warmup {args.warmup}, timing {args.steps} calls")
+    ms_call = time_calls(torch, fa_call, n_sets, args.steps, args.warmup)
+    kt = kernel_times(torch, xq, fa_call, n_sets, args.steps)
+    alg = cfg.algorithmic_bytes()
+    gbs = alg / (ms_call * 1e-3) / 1e9
+    p1_us = kt.get("fa_pass1", {}).get("avg_us", float("nan"))
+    # pass 1 moves all the algorithmic bytes except the output row (written by the reduce)
+    p1_bytes = alg - cfg.B * cfg.n_q * cfg.H * cfg.D * 4
+    p1_gbs = p1_bytes / (p1_us * 1e-6) / 1e9
+    log(f"FA: {ms_call * 1000:.2f} us/call, {gbs:.0f} GB/s; kernels {kt}")
+
+    # ---------------- GDN decode step
+    gcfg = wl.GDN_C3
+    g_sets_n = max(2, math.ceil(512 * 2**20 / gcfg.algorithmic_bytes()))
+    log(f"building {g_sets_n} GDN input sets")
+    gsets = make_gdn_sets(torch, xq, wl, gcfg, g_sets_n)
+
+    def gdn_call(i):
+        xq.gated_delta_net(*gsets[i], gcfg.slots, mode=xq.GDN_STEP)
+
+    g_ms = time_calls(torch, gdn_call, g_sets_n, max(args.steps, 100), args.warmup)
+    gkt = kernel_times(torch, xq, gdn_call, g_sets_n, max(args.steps, 100))
+    g_alg = gcfg.algorithmic_bytes()
+    g_kus = gkt.get("gdn_step", {}).get("avg_us", float("nan"))
+    log(f"GDN: {g_ms * 1000:.2f} us/call, kernel {g_kus:.2f} us")
+
+    # ---------------- CPU baselines (ggml-CPU semantics restated, this host's cores)
+    cpu = None
+    gdn_cpu = None
+    if not args.no_cpu:
+        try:
+            threads = len(os.sched_getaffinity(0))
+        except AttributeError:
+            threads = os.cpu_count() or 1
+        threads = max(1, min(threads, 16))
+        fa_call(0)
+        torch.cuda.synchronize()
+        log(f"CPU baseline: FA on {threads} threads")
+        t_cpu, n_cpu, max_err = cpu_fa_baseline(torch, wl, cfg, sets[0], threads, args.cpu_budget)
+        cpu = {"value": round(alg / t_cpu / 1e9, 3), "unit": "GB/s", "us_per_call": round(t_cpu * 1e6, 1),
+               "cores": threads, "kind": "port",
+               "sample": f"the full {cfg.name} call (same q8_0 bytes), oracle/xq_oracle.c ggml one-chunk loop, "
+                         f"median of {n_cpu} runs",
+               "gpu_vs_cpu_max_abs_err": max_err}
+        gdn_call(0)
+        torch.cuda.synchronize()
+        log(f"CPU baseline: GDN on {threads} threads")
+        t_g, n_g, g_err = cpu_gdn_baseline(torch, wl, gsets[0], gcfg.slots, threads, args.cpu_budget / 2)
+        gdn_cpu = {"us_per_call": round(t_g * 1e6, 1), "cores": threads, "kind": "port",
+                   "GB/s": round(g_alg / t_g / 1e9, 3), "median_of": n_g, "gpu_vs_cpu_max_abs_err": g_err}
+
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_call, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg.name, "op": "GGML_OP_FLASH_ATTN_EXT", "kv_type": "q8_0", "n_q": cfg.n_q,
+                   "n_head": cfg.H, "n_head_kv": cfg.Hkv, "head_dim": cfg.D, "kv_len": cfg.L,
+                   "n_seq": cfg.B, "mask": "f16 all-visible", "input_sets": n_sets,
+                   "compute": "int8 dot4 q8_0 scores, f32 online softmax and value accumulation"},
+        "us_per_call": round(ms_call * 1000, 2),
+        "pct_of_8TBs": round(100 * gbs / PEAK_GBS, 1),
+        "tokens_per_s_equiv": round(cfg.B * cfg.n_q / (ms_call * 1e-3), 1),
+        "algorithmic_bytes": alg,
+        "roofline": {"bound": "hbm", "kernel": "fa_pass1", "achieved": round(p1_gbs, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(p1_gbs / PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": p1_bytes, "avg_launch_us": round(p1_us, 3)},
+        "kernels": kt,
+        "cpu_baseline": cpu,
+        "gdn_step": {"workload": gcfg.name, "us_per_call": round(g_ms * 1000, 3),
+                     "kernel_avg_us": round(g_kus, 3), "algorithmic_bytes": g_alg,
+                     "GB/s": round(g_alg / (g_kus * 1e-6) / 1e9, 1),
+                     "frac": round(g_alg / (g_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
+                     "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1),
+                     "input_sets": g_sets_n, "cpu_baseline": gdn_cpu},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+"""GPU parity of GGML_OP_FLASH_ATTN_EXT (gfx950 kernels through the C ABI) against
+the ggml-CPU restatement in oracle/, at the benchmark configurations' full sizes.
+
+Tolerance (north star): max-abs 2e-3 / rel 1e-2 elementwise, f32 accumulation
+on the GPU; ggml's CPU path accumulates F16 V in an f16 vector, so the F16
+config is also compared with the float64 closed form as the tie-break.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle
+import xqattn
+from conftest import assert_close, case_note
+from fa_cases import dst_array, make_fa_case, oracle_f64, oracle_fa
+from xqattn import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(case, torch, qk_policy=xqattn.QK_CONSISTENT, split_mode=xqattn.SPLIT_AUTO, want_lse=True):
+    q = xqattn.DevTensor.from_host(case.q)
+    k = xqattn.DevTensor.from_host(case.k)
+    v = xqattn.DevTensor.from_host(case.v)
+    m = xqattn.DevTensor.from_host(case.mask) if case.mask is not None else None
+    s = xqattn.DevTensor.from_host(case.sinks) if case.sinks is not None else None
+    d = xqattn.DevTensor.empty_like_host(case.dst)
+    B, NQ, H, D = case.shape
+    lse = torch.empty(B * NQ * H, dtype=torch.float32, device="cuda") if want_lse else None
+    p = xqattn.fa_params(case.scale, case.max_bias, case.softcap, qk_policy, split_mode)
+    xqattn.flash_attn_ext(q, k, v, m, s, d, p, lse=lse)
+    torch.cuda.synchronize()
+    out = dst_array(case, d.to_host_bytes())
+    return out, (lse.cpu().numpy().reshape(B, NQ, H) if want_lse else None)
+
+
+@pytest.mark.parametrize("cfg", [wl.FA_C1, wl.FA_C2, wl.FA_C5], ids=lambda c: c.name)
+def test_fa_config_parity(torch_gpu, cfg):
+    case_note(f"flash_attn_ext {cfg.name}")
+    case = make_fa_case(cfg, seed=11)
+    got, glse = run_gpu(case, torch_gpu)
+    want, wlse = oracle_fa(case)
+    err = assert_close(got, want, what=f"{cfg.name} vs ggml-CPU restatement")
+    ref64, lse64 = oracle_f64(case)
+    err64 = assert_close(got, ref64, what=f"{cfg.name} vs float64 closed form")
+    assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what=f"{cfg.name} LSE")
+    print(f"{cfg.name}: max|gpu-ggml|={err:.2e} max|gpu-f64|={err64:.2e}")
+    if cfg.kv_type != wl.F16:
+        # f32 accumulation on both sides: only summation order differs
+        assert err64 < 1e-4
+
+
+@pytest.mark.parametrize("split_mode", [xqattn.SPLIT_REFERENCE, xqattn.SPLIT_FINE, xqattn.SPLIT_NONE,
+                                        xqattn.SPLIT_BALANCED, xqattn.SPLIT_COARSE])
+def test_fa_split_modes(torch_gpu, split_mode):
+    cfg = wl.FaConfig("q8_split", 1, 24, 4, 256, 5000, 2, wl.Q8_0)
+    case_note(f"split mode {split_mode}")
+    case = make_fa_case(cfg, seed=3)
+    got, _ = run_gpu(case, torch_gpu, split_mode=split_mode)
+    ref64, _ = oracle_f64(case)
+    assert_close(got, ref64, atol=1e-4, rtol=1e-4, what=f"split {split_mode}")
+    again, _ = run_gpu(case, torch_gpu, split_mode=split_mode)
+    assert np.array_equal(got, again), "not deterministic"
+
+
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2])
+@pytest.mark.parametrize("D,H,Hkv", [(128, 32, 8), (256, 24, 4), (128, 16, 16)])
+def test_fa_query_width_invariance(torch_gpu, kv_type, D, H, Hkv):
+    """A query's result is bitwise the same alone (n_q = 1) or inside an n_q <= 8 batch."""
+    cfg = wl.FaConfig("inv", 8, H, Hkv, D, 1000, 2, kv_type, causal_prefix=992)
+    case_note(f"invariance {wl.TYPE_NAME[kv_type]} D{D} H{H}/{Hkv}")
+    case = make_fa_case(cfg, seed=5)
+    batch, _ = run_gpu(case, torch_gpu)
+    q_all = np.frombuffer(case.q.buf.tobytes(), np.float32).reshape(2, 8, H, D)
+    m_all = np.frombuffer(case.mask.buf.tobytes(), np.uint16).reshape(1, 8, 1000)
+    cfg1 = wl.FaConfig("inv1", 1, H, Hkv, D, 1000, 2, kv_type)
+    for i in (0, 3, 7):
+        single = dataclasses.replace(case, cfg=cfg1, q=wl.fa_q_tensor(q_all[:, i:i + 1].copy()),
+                                     mask=wl.mask_tensor(m_all[:, i:i + 1].copy()),
+                                     dst=wl.fa_dst_tensor(2, 1, H, D))
+        one, _ = run_gpu(single, torch_gpu)
+        assert np.array_equal(one[:, 0], batch[:, i]), f"query {i} differs between n_q=1 and n_q=8"
+
+
+def test_fa_padding_rows_and_fully_masked(torch_gpu):
+    """Extra query rows whose mask rows are all -inf produce 0 and LSE -inf."""
+    cfg = wl.FaConfig("pad", 10, 32, 8, 128, 700, 2, wl.Q4_0, causal_prefix=692, n_q_pad=16)
+    case = make_fa_case(cfg, seed=9)
+    m = wl.fa_causal_mask(cfg, n_q_rows=8)  # rows 8..15 all -inf
+    case.mask = wl.mask_tensor(m)
+    got, lse = run_gpu(case, torch_gpu)
+    want, wlse = oracle_fa(case)
+    assert np.all(got[:, 8:] == 0.0)
+    assert np.all(np.isneginf(lse[:, 8:]))
+    assert_close(got, want, what="padded verify")
+
+
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2])
+def test_fa_sinks_softcap_alibi(torch_gpu, kv_type):
+    cfg = wl.FaConfig("feat", 3, 12, 4, 128, 900, 2, kv_type, causal_prefix=897)
+    case = make_fa_case(cfg, seed=21, sinks=True, softcap=30.0, max_bias=8.0, mask_per_seq=True)
+    got, glse = run_gpu(case, torch_gpu)
+    want, wlse = oracle_fa(case)
+    assert_close(got, want, what="sinks+softcap+alibi vs ggml restatement")
+    ref64, lse64 = oracle_f64(case)
+    assert_close(got, ref64, what="sinks+softcap+alibi vs f64")
+    assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what="lse")
+
+
+def test_fa_native_policy_f16(torch_gpu):
+    cfg = wl.FaConfig("native", 2, 16, 8, 128, 1500, 1, wl.F16, causal_prefix=1498)
+    case = make_fa_case(cfg, seed=4)
+    got, _ = run_gpu(case, torch_gpu, qk_policy=xqattn.QK_NATIVE)
+    want, _ = oracle_fa(case, policy=oracle.QK_NATIVE)
+    assert_close(got, want, what="native f16 policy")
+    ref64, _ = oracle_f64(case, policy=oracle.QK_NATIVE, q_round=True)
+    assert_close(got, ref64, atol=1e-5, rtol=1e-4, what="native f16 vs f64 (f16-rounded Q)")
+
+
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2])
+@pytest.mark.parametrize("D", [128, 256])
+def test_kv_store_bit_exact(torch_gpu, kv_type, D):
+    """GPU KV append quantizers are bit-identical to ggml's (oracle restatement)."""
+    torch = torch_gpu
+    n_tok, hkv, cap = 37, 4, 64
+    x = wl.normal(77, (n_tok, hkv, D)) * np.float32(3.0)
+    x[0, 0, :5] = [0.0, -0.0, 65504.0, 1e-8, -7.5]       # edge values
+    x[1, 1, :] = 0.0                                        # all-zero block -> d = 0
+    pos = np.array([(5 * i + 3) % cap for i in range(n_tok)], np.int32)
+    pos[-1] = cap + 5                                        # out of range: skipped
+    rec = wl.record_bytes(kv_type, D)
+    for variant in (0, 1) if kv_type == wl.Q8_0 else (0,):
+        want = np.zeros((cap, hkv, rec), np.uint8)
+        oracle.kv_store(x, pos, hkv, D, kv_type, want, cap, variant)
+        dst = torch.zeros(cap * hkv * rec, dtype=torch.uint8, device="cuda")
+        xqattn.kv_store(torch.from_numpy(x).cuda(), torch.from_numpy(pos).cuda(), hkv, D, kv_type, dst, cap,
+                        q8_variant=variant)
+        torch.cuda.synchronize()
+        got = dst.cpu().numpy().reshape(cap, hkv, rec)
+        assert np.array_equal(got, want), f"kv_store {wl.TYPE_NAME[kv_type]} D{D} variant {variant}"
+
+
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0])
+@pytest.mark.parametrize("active", [0, 1, 64, 257, 4096])
+def test_fa_range_vs_reference_semantics(torch_gpu, kv_type, active):
+    """attend_range: causal limits from positions/origin, empty -> O=0, LSE=-inf."""
+    torch = torch_gpu
+    n_head, hkv, D, origin = 24, 4, 256, 102400
+    cap = max(active, 1)
+    kf = wl.normal(31, (cap, hkv, D))
+    vf = wl.normal(32, (cap, hkv, D))
+    kraw = oracle.quantize(kv_type, kf)
+    vraw = oracle.quantize(kv_type, vf)
+    positions = np.array([origin + active - 1, origin - 5, origin + active // 2, origin + active + 100], np.int32)
+    q = wl.normal(33, (4, n_head, D))
+    scale = 1.0 / 16
+    split_k = oracle.load().xo_ref_split_k(active)
+    want, wlse, _ = oracle.range_attn(q, positions, n_head, kraw, vraw, hkv, D, kv_type, origin, active, scale, split_k)
+    out = torch.empty(4 * n_head * D, dtype=torch.float32, device="cuda")
+    lse = torch.empty(4 * n_head, dtype=torch.float32, device="cuda")
+    xqattn.fa_range(torch.from_numpy(q).cuda(), torch.from_numpy(positions).cuda(), n_head,
+                    torch.from_numpy(kraw.reshape(-1)).cuda(), torch.from_numpy(vraw.reshape(-1)).cuda(),
+                    hkv, D, kv_type, origin, active, scale, out, lse)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(4, n_head, D)
+    glse = lse.cpu().numpy().reshape(4, n_head)
+    # reference GPU tolerance: 3e-4 + 3e-4|ref| (O), 3e-4 + 3e-5|ref| (LSE)
+    assert_close(got, want, atol=3e-4, rtol=3e-4, what="range O")
+    assert_close(glse, wlse, atol=3e-4, rtol=3e-5, what="range LSE")
+    assert np.all(got[1] == 0.0) and np.all(np.isneginf(glse[1])), "query before origin must be empty"

@@ -1,0 +1,108 @@
+// xq_kernels.h — internal launch interface between the C-ABI layer (xq_api.hip)
+// and the gfx950 kernels. Shapes arrive here already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "xq_attn.h"
+#include "xq_device.h"
+
+namespace xq {
+
+// Brackets one kernel launch with HIP events while profiling is enabled.
+class ProfScope {
+  public:
+    ProfScope(const char* name, hipStream_t stream);
+    ~ProfScope();
+    ProfScope(const ProfScope&) = delete;
+    ProfScope& operator=(const ProfScope&) = delete;
+
+  private:
+    const char* name_;
+    hipStream_t stream_;
+    hipEvent_t start_{}, stop_{};
+    bool active_ = false;
+};
+
+// ---------------------------------------------------------------- storage
+
+constexpr int kQK = 32;  // elements per q8_0 / q4_0 block
+
+constexpr int rec_bytes(int kt, int d) {
+    return kt == XQ_TYPE_F16 ? 2 * d
+         : kt == XQ_TYPE_Q8_0 ? d / kQK * 34
+         : kt == XQ_TYPE_Q4_0 ? d / kQK * 18
+         : kt == XQ_TYPE_E5M2 ? d
+         : kt == XQ_TYPE_F32 ? 4 * d
+         : 0;
+}
+
+// ---------------------------------------------------------------- flash attn
+
+// Score mode: float image (f32 Q, or Q rounded to f16) against decoded K, or
+// q8_0 image against quantized K with integer block dots.
+enum QkMode { kQkFloat = 0, kQkInt8 = 1 };
+
+// 32-bit words of one Q image row (one query x head).
+constexpr int qimg_words(int qkm, int kt, int d) {
+    return qkm == kQkFloat ? d
+         : kt == XQ_TYPE_Q8_0 ? (d / 64) * 17 + d / kQK         // pair images + d_q
+         : (d / 64) * 18 + 2 * (d / kQK);                        // lo/hi images + d_q + sum_q
+}
+
+struct FaLaunch {
+    const xq_tensor* q;
+    const xq_tensor* k;
+    const xq_tensor* v;
+    const xq_tensor* mask;   // may be null
+    const xq_tensor* sinks;  // may be null
+    const xq_tensor* dst;
+    float* lse;              // may be null
+    float scale, max_bias, softcap;
+    int qk_mode;             // QkMode
+    int q_round_f16;         // float image rounded to f16 (NATIVE policy, F16 K)
+    int n_splits;
+    int64_t split_rows;
+    int poison;              // reduce poisons non-finite partial states
+    // range mode (positions != null): row r visible to query i iff
+    // r < min(active, positions[i] - origin + 1); kv_len == active.
+    const int32_t* positions;
+    int32_t origin;
+    void* workspace;
+    size_t workspace_bytes;
+};
+
+size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits);
+hipError_t fa_launch(const FaLaunch& L, hipStream_t stream);
+// Whether a compiled kernel exists for this combination.
+bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs);
+
+// ---------------------------------------------------------------- gdn
+
+struct GdnLaunch {
+    const xq_tensor* q;
+    const xq_tensor* k;
+    const xq_tensor* v;
+    const xq_tensor* g;
+    const xq_tensor* beta;
+    const xq_tensor* state;
+    const xq_tensor* dst;
+    int32_t slots;
+    void* workspace;
+    size_t workspace_bytes;
+};
+
+hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream);
+size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B);
+hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream);
+bool gdn_chunked_available();
+
+// ---------------------------------------------------------------- kv append
+
+hipError_t kv_store_launch(const float* src, const int32_t* positions, int32_t n_tokens,
+                           int32_t n_head_kv, int32_t head_dim, int32_t kv_type,
+                           int32_t q8_variant, void* dst, int32_t capacity, hipStream_t stream);
+
+}  // namespace xq
