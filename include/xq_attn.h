@@ -107,13 +107,25 @@ enum xq_fa_split_mode {
     XQ_FA_SPLIT_NONE = 5,
 };
 
+/* Which pass-1 kernel computes the scores and the value product.
+ *  XQ_FA_ENGINE_AUTO: the matrix-core kernel where it exists (q8_0/q4_0 K with
+ *    integer scores, F16/E5M2 K), else the VALU kernel.
+ *  XQ_FA_ENGINE_MFMA: the matrix-core kernel (UNSUPPORTED where it does not exist).
+ *  XQ_FA_ENGINE_VALU: the vector-ALU kernel (dot4 integer scores, f32 FMA values). */
+enum xq_fa_engine {
+    XQ_FA_ENGINE_AUTO = 0,
+    XQ_FA_ENGINE_MFMA = 1,
+    XQ_FA_ENGINE_VALU = 2,
+};
+
 typedef struct xq_fa_params {
     float scale;         /* op_params[0] */
     float max_bias;      /* op_params[1], ALiBi; 0 = off */
     float logit_softcap; /* op_params[2]; 0 = off */
     int32_t qk_policy;   /* enum xq_fa_qk_policy */
     int32_t split_mode;  /* enum xq_fa_split_mode */
-    int32_t reserved[3];
+    int32_t engine;      /* enum xq_fa_engine */
+    int32_t reserved[2];
 } xq_fa_params;
 
 /* Pure predicate mirroring a ggml backend's supports_op for

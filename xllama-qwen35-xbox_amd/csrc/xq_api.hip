@@ -134,6 +134,8 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
         return fail(XQ_ERR_BAD_ARG, "bad qk_policy %d", p->qk_policy);
     if (p->split_mode < XQ_FA_SPLIT_AUTO || p->split_mode > XQ_FA_SPLIT_NONE)
         return fail(XQ_ERR_BAD_ARG, "bad split_mode %d", p->split_mode);
+    if (p->engine < XQ_FA_ENGINE_AUTO || p->engine > XQ_FA_ENGINE_VALU)
+        return fail(XQ_ERR_BAD_ARG, "bad engine %d", p->engine);
     for (int i = 0; i < 4; ++i)
         if (q->ne[i] < 1 || k->ne[i] < 0 || v->ne[i] < 0 || dst->ne[i] < 1)
             return fail(XQ_ERR_BAD_SHAPE, "bad ne");
@@ -185,8 +187,11 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
     P.q_round_f16 = (p->qk_policy == XQ_FA_QK_NATIVE && k->type == XQ_TYPE_F16) ? 1 : 0;
     split_policy(P.L, p->split_mode, &P.n_splits, &P.split_rows);
     if (P.n_splits > 256) return fail(XQ_ERR_UNSUPPORTED, "more than 256 KV splits");
-    if (!xq::fa_kernel_available(P.kt, P.D, P.qk_mode, P.G * (P.NQ < 32 / P.G ? P.NQ : 32 / P.G)))
+    const int npairs = P.G * (P.NQ < 32 / P.G ? P.NQ : 32 / P.G);
+    if (!xq::fa_kernel_available(P.kt, P.D, P.qk_mode, npairs))
         return fail(XQ_ERR_UNSUPPORTED, "no kernel for this combination");
+    if (p->engine == XQ_FA_ENGINE_MFMA && !xq::fa_mma_available(P.kt, P.D, P.qk_mode, npairs))
+        return fail(XQ_ERR_UNSUPPORTED, "no matrix-core kernel for this combination");
     P.ws = xq::fa_workspace_bytes((int64_t)B * NQ * H, P.D, P.qk_mode, P.kt, P.n_splits);
     if (plan) *plan = P;
     return XQ_OK;
@@ -268,6 +273,7 @@ xq_status xq_flash_attn_ext(const xq_tensor* q, const xq_tensor* k, const xq_ten
     L.n_splits = P.n_splits;
     L.split_rows = P.split_rows;
     L.poison = 0;
+    L.engine = params->engine;
     L.positions = nullptr;
     L.origin = 0;
     L.workspace = workspace;
@@ -343,6 +349,7 @@ xq_status xq_fa_range(const float* q, const int32_t* positions, int32_t n_q, int
     L.n_splits = P.n_splits;
     L.split_rows = P.split_rows;
     L.poison = 1;
+    L.engine = XQ_FA_ENGINE_AUTO;
     L.positions = positions;
     L.origin = origin;
     L.workspace = workspace;

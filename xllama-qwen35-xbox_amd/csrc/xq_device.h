@@ -58,6 +58,27 @@ XQ_DEV float row16_max(float x) {
     x = fmaxf(x, dpp<0x140>(x));
     return x;
 }
+template <int CTRL>
+XQ_DEV int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+// Order-preserving float <-> int map (valid for every non-NaN float): integer
+// max then equals float max, without the IEEE canonicalisation fmaxf needs.
+XQ_DEV int f2ord(float x) {
+    const int i = __float_as_int(x);
+    return i >= 0 ? i : i ^ 0x7fffffff;
+}
+XQ_DEV float ord2f(int i) { return __int_as_float(i >= 0 ? i : i ^ 0x7fffffff); }
+// Row-of-16 maximum (exact) via integer DPP max.
+XQ_DEV float row16_max_ord(float x) {
+    int i = f2ord(x);
+    i = max(i, dpp_i<0xB1>(i));
+    i = max(i, dpp_i<0x4E>(i));
+    i = max(i, dpp_i<0x141>(i));
+    i = max(i, dpp_i<0x140>(i));
+    return ord2f(i);
+}
+
 XQ_DEV float lane_read(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }

@@ -26,84 +26,9 @@
 // call (the purpose of patches/0006-…:7-11 and patches/0008-…:40-56). The
 // kernels are compiled with -ffp-contract=off and write every fused
 // multiply-add explicitly.
-#include "xq_kernels.h"
-
-#include <math.h>
+#include "xq_fa_common.h"
 
 namespace xq {
-
-constexpr int kTile = 64;
-constexpr int kThreads = 256;
-constexpr int kMaxSplits = 256;
-
-// LDS record stride: a multiple of 16 bytes with an odd number of 16-byte
-// units, so 16 lanes reading 16 bytes from consecutive records hit distinct
-// bank groups.
-constexpr int pad_rec(int rec) {
-    int u = (rec + 15) / 16;
-    if ((u & 1) == 0) ++u;
-    return u * 16;
-}
-constexpr int chunk_bytes(int rec) { return rec % 16 == 0 ? 16 : rec % 8 == 0 ? 8 : 4; }
-
-template <int CH> struct ChunkT;
-template <> struct ChunkT<16> { using T = uint4; };
-template <> struct ChunkT<8> { using T = uint2; };
-template <> struct ChunkT<4> { using T = uint32_t; };
-
-struct FaArgs {
-    const uint8_t* k;
-    const uint8_t* v;
-    int64_t k_nb1, k_nb2, k_nb3;
-    int64_t v_nb1, v_nb2, v_nb3;
-    const uint8_t* mask;
-    int64_t m_nb1, m_nb2, m_nb3;
-    int32_t m_ne2, m_ne3;
-    const int32_t* positions;
-    int32_t origin;
-    const float* sinks;
-    uint8_t* dst;
-    int64_t d_nb1, d_nb2, d_nb3;
-    float* lse;
-    float* part_o;
-    float2* part_ml;
-    int64_t L;
-    int64_t split_rows;
-    int32_t H, Hkv, G, NQ, B, QT, n_qtiles, n_splits, rk3, rv3;
-    float scale, softcap, max_bias, m0, m1;
-    int32_t n_head_log2;
-    int32_t poison;
-};
-
-XQ_DEV float alibi_slope(const FaArgs& a, int h) {
-    if (!(a.max_bias > 0.0f)) return 1.0f;
-    return h < a.n_head_log2 ? powf(a.m0, (float)(h + 1))
-                             : powf(a.m1, (float)(2 * (h - a.n_head_log2) + 1));
-}
-
-// Sinks and 1/S exactly as ggml's tail of the one-chunk loop: a sink above the
-// running maximum rescales the accumulator by exp(M - sink) and adds 1 to S,
-// otherwise S += exp(sink - M); then out = acc * (S == 0 ? 0 : 1/S).
-XQ_DEV void fa_finalize(float M, float S, bool has_sink, float sink, float& a1, float& inv,
-                        float& lse) {
-    a1 = 1.0f;
-    float meff = M;
-    if (has_sink) {
-        if (sink > M) {
-            const float ms = expf(M - sink);
-            a1 = ms;
-            S = fmaf(S, ms, 1.0f);
-            meff = sink;
-        } else {
-            S = S + expf(sink - M);
-        }
-    }
-    inv = S == 0.0f ? 0.0f : 1.0f / S;
-    lse = S > 0.0f ? meff + logf(S) : -INFINITY;
-}
-
-XQ_DEV uint32_t lds_u32(const uint8_t* p) { return *(const uint32_t*)p; }
-XQ_DEV uint32_t lds_u16(const uint8_t* p) { return *(const uint16_t*)p; }
 
 // Decode VD consecutive elements starting at element e0 (multiple of VD) of a
 // record in LDS. Bit-exact ggml decoders: f16 -> f32; q8_0 qs*d; q4_0
@@ -441,8 +366,8 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
                 s = valid ? s : -INFINITY;
                 const float tmax = wave_max(s);
                 const float m_new = fmaxf(m_run[u], tmax);
-                const float alpha = m_new == -INFINITY ? 1.0f : expf(m_run[u] - m_new);
-                const float pr = s == -INFINITY ? 0.0f : expf(s - m_new);
+                const float alpha = m_new == -INFINITY ? 1.0f : fast_exp(m_run[u] - m_new);
+                const float pr = s == -INFINITY ? 0.0f : fast_exp(s - m_new);
                 l_run[u] = fmaf(l_run[u], alpha, wave_sum(pr));
                 m_run[u] = m_new;
                 sP[lane * PS + p] = pr;
@@ -553,11 +478,13 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
 }
 
 // One workgroup of D threads per (sequence, query, head) row; thread d owns
-// output dim d and sums the splits in ascending order.
+// output dim d and sums the splits in ascending order. The split states are
+// loaded in parallel; the partial numerators are fetched 16 splits at a time
+// so the loads are in flight together while the sum keeps its order.
 template <int D>
 __global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
     __shared__ float sm[kMaxSplits], sl[kMaxSplits], sw[kMaxSplits];
-    __shared__ float sA1, sInv;
+    __shared__ float sA1, sInv, sMax[D / 64];
     __shared__ int sBad;
     const int64_t row = blockIdx.x;
     const int S = a.n_splits;
@@ -565,41 +492,52 @@ __global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
     const int b = (int)(row / rows_per_seq);
     const int h = (int)(row % a.H);
+    float mloc = -3.402823466e38f;
+    int bad = 0;
     for (int s = d; s < S; s += D) {
         const float2 ml = a.part_ml[row * S + s];
         sm[s] = ml.x;
         sl[s] = ml.y;
-    }
-    __syncthreads();
-    if (d == 0) {
-        int bad = 0;
-        float M = -3.402823466e38f;
-        for (int s = 0; s < S; ++s) {
-            const float l = sl[s];
-            if (l == 0.0f) continue;
-            if (!isfinite(l) || l < 0.0f || !isfinite(sm[s]))
+        if (ml.y != 0.0f) {
+            if (!isfinite(ml.y) || ml.y < 0.0f || !isfinite(ml.x))
                 bad = 1;
             else
-                M = fmaxf(M, sm[s]);
+                mloc = fmaxf(mloc, ml.x);
         }
-        for (int s = 0; s < S; ++s) sw[s] = sl[s] != 0.0f ? expf(sm[s] - M) : 0.0f;
+    }
+    mloc = wave_max(mloc);
+    if (lane_id() == 0) sMax[d / 64] = mloc;
+    bad = __syncthreads_or(bad);
+    float M = sMax[0];
+#pragma unroll
+    for (int w = 1; w < D / 64; ++w) M = fmaxf(M, sMax[w]);
+    for (int s = d; s < S; s += D) sw[s] = sl[s] != 0.0f ? expf(sm[s] - M) : 0.0f;
+    __syncthreads();
+    if (d == 0) {
         float L = 0.0f;
         for (int s = 0; s < S; ++s)
             if (sl[s] != 0.0f) L = fmaf(sl[s], sw[s], L);
-        if (!isfinite(L)) bad = 1;
+        int badl = bad || !isfinite(L);
         float a1, inv, lse;
         fa_finalize(L == 0.0f ? -INFINITY : M, L, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
-        if (!isfinite(inv) || (L != 0.0f && !isfinite(lse))) bad = 1;
+        if (!isfinite(inv) || (L != 0.0f && !isfinite(lse))) badl = 1;
         sA1 = a1;
         sInv = inv;
-        sBad = bad && a.poison;
-        if (a.lse) a.lse[row] = (bad && a.poison) ? NAN : lse;
+        sBad = badl && a.poison;
+        if (a.lse) a.lse[row] = (badl && a.poison) ? NAN : lse;
     }
     __syncthreads();
     const float* po = a.part_o + row * S * D + d;
     float acc = 0.0f;
-    for (int s = 0; s < S; ++s)
-        if (sl[s] != 0.0f) acc = fmaf(po[(int64_t)s * D], sw[s], acc);
+    constexpr int CH = 16;
+    for (int s0 = 0; s0 < S; s0 += CH) {
+        float v[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) v[i] = (s0 + i < S) ? po[(int64_t)(s0 + i) * D] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < CH; ++i)
+            if (s0 + i < S && sl[s0 + i] != 0.0f) acc = fmaf(v[i], sw[s0 + i], acc);
+    }
     float out = (acc * sA1) * sInv;
     if (a.poison) {
         // any non-finite participating state or numerator poisons the whole row
@@ -764,8 +702,14 @@ bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+static size_t qimg_bytes(int64_t n_rows, int d, int qk_mode, int kt) {
+    size_t b = (size_t)n_rows * qimg_words(qk_mode, kt, d) * 4;
+    const size_t m = fa_mma_qimg_bytes(n_rows, kt, d);
+    return b > m ? b : m;
+}
+
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits) {
-    size_t bytes = align256((size_t)n_rows * qimg_words(qk_mode, kt, d) * 4);
+    size_t bytes = align256(qimg_bytes(n_rows, d, qk_mode, kt));
     if (n_splits > 1) {
         bytes += align256((size_t)n_rows * n_splits * d * 4);
         bytes += align256((size_t)n_rows * n_splits * 8);
@@ -825,20 +769,25 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
     a.QT = QT;
     a.n_qtiles = (NQ + QT - 1) / QT;
     const int np = np_bin(QT * G);
-    Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);
-    QprepFn qp = D == 128 ? qprep_d<128>(kt, L.qk_mode) : qprep_d<256>(kt, L.qk_mode);
-    if (!p1 || !qp) return hipErrorInvalidValue;
-
     const int64_t n_rows = (int64_t)B * NQ * H;
     uint8_t* ws = (uint8_t*)L.workspace;
     uint32_t* qimg = (uint32_t*)ws;
-    size_t off = align256((size_t)n_rows * qimg_words(L.qk_mode, kt, D) * 4);
+    size_t off = align256(qimg_bytes(n_rows, D, L.qk_mode, kt));
     if (L.n_splits > 1) {
         a.part_o = (float*)(ws + off);
         off += align256((size_t)n_rows * L.n_splits * D * 4);
         a.part_ml = (float2*)(ws + off);
     }
 
+    const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G);
+    if (L.engine == XQ_FA_ENGINE_MFMA && !mma) return hipErrorInvalidValue;
+    if (mma) {
+        hipError_t e = fa_mma_launch(a, L, (uint8_t*)qimg, stream);
+        if (e != hipSuccess) return e;
+    } else {
+    Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);
+    QprepFn qp = D == 128 ? qprep_d<128>(kt, L.qk_mode) : qprep_d<256>(kt, L.qk_mode);
+    if (!p1 || !qp) return hipErrorInvalidValue;
     {
         ProfScope ps("fa_qprep", stream);
         hipLaunchKernelGGL(qp, dim3((uint32_t)n_rows), dim3(64), 0, stream, (const uint8_t*)q->data,
@@ -848,6 +797,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
     {
         ProfScope ps("fa_pass1", stream);
         hipLaunchKernelGGL(p1, dim3(n_wg), dim3(kThreads), 0, stream, a, (const uint32_t*)qimg);
+    }
     }
     if (L.n_splits > 1) {
         ProfScope ps("fa_reduce", stream);

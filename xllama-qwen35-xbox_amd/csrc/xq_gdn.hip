@@ -11,6 +11,8 @@
 // and each kept snapshot written once.
 #include "xq_kernels.h"
 
+#include <stdlib.h>
+
 namespace xq {
 
 struct GdnStepArgs {
@@ -42,23 +44,52 @@ XQ_DEV float ld_elem(const uint8_t* p, int i) {
         return ((const float*)p)[i];
 }
 
-constexpr int kGdnColsPerWg = 16;
+// Eight elements i = 64*r + 4*li + j (r, j in 0..1, 0..3) of a q/k row.
+template <bool BF16, bool VEC>
+XQ_DEV void ld_row8(const uint8_t* p, int li, float (&x)[8]) {
+    if constexpr (VEC && !BF16) {
+        const float4 a = *(const float4*)(p + 16 * li);
+        const float4 b = *(const float4*)(p + 256 + 16 * li);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else if constexpr (VEC && BF16) {
+        const uint2 a = *(const uint2*)(p + 8 * li);
+        const uint2 b = *(const uint2*)(p + 128 + 8 * li);
+        const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = bf16_bits_to_f32(w[e] & 0xffffu);
+            x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) x[4 * r + j] = ld_elem<BF16>(p, 64 * r + 4 * li + j);
+    }
+}
 
-template <bool BF16>
+// CPT state columns per 16-lane row (column c_j = base + row + 16*j); their
+// state loads are all issued before any compute so they are in flight together.
+template <bool BF16, bool VEC, int CPT>
 __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
-    const int n_wg = a.B * 32 * (128 / kGdnColsPerWg);
+    constexpr int COLS = 16 * CPT;  // columns per workgroup
+    const int n_wg = a.B * 32 * (128 / COLS);
     const int wg = (int)xcd_remap(blockIdx.x, (uint32_t)n_wg);
-    const int cblk = wg % (128 / kGdnColsPerWg);
-    const int bh = wg / (128 / kGdnColsPerWg);
+    const int cblk = wg % (128 / COLS);
+    const int bh = wg / (128 / COLS);
     const int b = bh / 32, h = bh % 32, kh = h % 16;
-    const int lane = lane_id();
-    const int li = lane & 15;
-    const int col = cblk * kGdnColsPerWg + (int)(threadIdx.x >> 4);
+    const int li = threadIdx.x & 15;
+    const int col0 = cblk * COLS + (int)(threadIdx.x >> 4);
 
-    const float* s_in = (const float*)((const char*)a.state + (int64_t)b * a.s_nb3) +
-                        ((int64_t)h * 128 + col) * 128;
-    float4 s0 = *(const float4*)(s_in + 4 * li);
-    float4 s1 = *(const float4*)(s_in + 64 + 4 * li);
+    const float* s_in = (const float*)((const char*)a.state + (int64_t)b * a.s_nb3) + (int64_t)h * 16384;
+    float4 s0[CPT], s1[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const float* sc = s_in + (int64_t)(col0 + 16 * j) * 128;
+        s0[j] = *(const float4*)(sc + 4 * li);
+        s1[j] = *(const float4*)(sc + 64 + 4 * li);
+    }
 
     float* out = (float*)((char*)a.dst + (int64_t)b * a.dst_nb2);
     const int64_t s_off = (int64_t)4096 * a.T;
@@ -67,46 +98,63 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
         const uint8_t* qp = a.q + (int64_t)b * a.q_nb3 + (int64_t)t * a.q_nb2 + (int64_t)kh * a.q_nb1;
         const uint8_t* kp = a.k + (int64_t)b * a.k_nb3 + (int64_t)t * a.k_nb2 + (int64_t)kh * a.k_nb1;
         float qv[8], kv[8];
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qv[4 * r + j] = ld_elem<BF16>(qp, 64 * r + 4 * li + j);
-                kv[4 * r + j] = ld_elem<BF16>(kp, 64 * r + 4 * li + j);
-            }
+        ld_row8<BF16, VEC>(qp, li, qv);
+        ld_row8<BF16, VEC>(kp, li, kv);
         const float gt = *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)t * a.g_nb2 + (int64_t)h * a.g_nb1);
         const float bt = *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)t * a.b_nb2 + (int64_t)h * a.b_nb1);
-        const float vt = ld_elem<BF16>(a.v + (int64_t)b * a.v_nb3 + (int64_t)t * a.v_nb2 + (int64_t)h * a.v_nb1, col);
+        const uint8_t* vrow = a.v + (int64_t)b * a.v_nb3 + (int64_t)t * a.v_nb2 + (int64_t)h * a.v_nb1;
         const float decay = expf(gt);
-
-        float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        float part = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            s[e] = s[e] * decay;
-            part = fmaf(s[e], kv[e], part);
-        }
-        const float dot_sk = row16_sum(part);
-        const float delta = (vt - dot_sk) * bt;
-        float att = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            s[e] = fmaf(kv[e], delta, s[e]);
-            att = fmaf(s[e], qv[e], att);
-        }
-        const float y = row16_sum(att);
-        if (li == 0) out[((int64_t)t * 32 + h) * 128 + col] = y * a.scale;
-        s0 = make_float4(s[0], s[1], s[2], s[3]);
-        s1 = make_float4(s[4], s[5], s[6], s[7]);
-
         const int slot = a.T - 1 - t;
-        if ((a.slots > 1 && slot < a.slots) || (a.slots == 1 && t + 1 == a.T)) {
-            float* snap = out + s_off + (int64_t)(a.slots == 1 ? 0 : slot) * 524288 +
-                          ((int64_t)h * 128 + col) * 128;
-            *(float4*)(snap + 4 * li) = s0;
-            *(float4*)(snap + 64 + 4 * li) = s1;
+        const bool keep = (a.slots > 1 && slot < a.slots) || (a.slots == 1 && t + 1 == a.T);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int col = col0 + 16 * j;
+            const float vt = ld_elem<BF16>(vrow, col);
+            float s[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w, s1[j].x, s1[j].y, s1[j].z, s1[j].w};
+            float part = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                s[e] = s[e] * decay;
+                part = fmaf(s[e], kv[e], part);
+            }
+            const float dot_sk = row16_sum(part);
+            const float delta = (vt - dot_sk) * bt;
+            float att = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                s[e] = fmaf(kv[e], delta, s[e]);
+                att = fmaf(s[e], qv[e], att);
+            }
+            const float y = row16_sum(att);
+            if (li == 0) out[((int64_t)t * 32 + h) * 128 + col] = y * a.scale;
+            s0[j] = make_float4(s[0], s[1], s[2], s[3]);
+            s1[j] = make_float4(s[4], s[5], s[6], s[7]);
+            if (keep) {
+                float* snap = out + s_off + (int64_t)(a.slots == 1 ? 0 : slot) * 524288 + ((int64_t)h * 128 + col) * 128;
+                *(float4*)(snap + 4 * li) = s0[j];
+                *(float4*)(snap + 64 + 4 * li) = s1[j];
+            }
         }
     }
+}
+
+template <bool BF16, bool VEC>
+static void gdn_step_dispatch(int cpt, int B, hipStream_t stream, const GdnStepArgs& a) {
+    switch (cpt) {
+    case 1: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 1>), dim3(B * 32 * 8), dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 2>), dim3(B * 32 * 4), dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 4>), dim3(B * 32 * 2), dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 8>), dim3(B * 32 * 1), dim3(256), 0, stream, a); break;
+    }
+}
+
+static int gdn_cpt() {
+    static int cpt = [] {
+        const char* e = getenv("XQ_GDN_CPT");
+        const int v = e ? atoi(e) : 2;
+        return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 2;
+    }();
+    return cpt;
 }
 
 hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
@@ -129,12 +177,22 @@ hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
     a.B = (int32_t)L.v->ne[3];
     a.slots = L.slots;
     a.scale = 1.0f / sqrtf(128.0f);
-    const int n_wg = a.B * 32 * (128 / kGdnColsPerWg);
+    const bool bf16 = L.q->type == XQ_TYPE_BF16;
+    const size_t al = bf16 ? 8 : 16;  // q/k rows read as 16- (f32) or 8-byte (bf16) vectors
+    bool vec = true;
+    for (const xq_tensor* t : {L.q, L.k}) {
+        vec = vec && ((uintptr_t)t->data % al == 0);
+        for (int i = 1; i < 4; ++i) vec = vec && (t->nb[i] % al == 0);
+    }
+    const int cpt = gdn_cpt();
     ProfScope ps("gdn_step", stream);
-    if (L.q->type == XQ_TYPE_BF16)
-        hipLaunchKernelGGL(gdn_step_kernel<true>, dim3(n_wg), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(gdn_step_kernel<false>, dim3(n_wg), dim3(256), 0, stream, a);
+    if (bf16) {
+        if (vec) gdn_step_dispatch<true, true>(cpt, a.B, stream, a);
+        else gdn_step_dispatch<true, false>(cpt, a.B, stream, a);
+    } else {
+        if (vec) gdn_step_dispatch<false, true>(cpt, a.B, stream, a);
+        else gdn_step_dispatch<false, false>(cpt, a.B, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -66,6 +66,7 @@ struct FaLaunch {
     int n_splits;
     int64_t split_rows;
     int poison;              // reduce poisons non-finite partial states
+    int engine;              // xq_fa_engine
     // range mode (positions != null): row r visible to query i iff
     // r < min(active, positions[i] - origin + 1); kv_len == active.
     const int32_t* positions;
@@ -78,6 +79,8 @@ size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_spli
 hipError_t fa_launch(const FaLaunch& L, hipStream_t stream);
 // Whether a compiled kernel exists for this combination.
 bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs);
+bool fa_mma_available(int kt, int d, int qk_mode, int n_pairs);
+size_t fa_mma_qimg_bytes(int64_t n_rows, int kt, int d);
 
 // ---------------------------------------------------------------- gdn
 

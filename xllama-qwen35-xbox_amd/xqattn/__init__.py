@@ -32,6 +32,7 @@ STATUS = {0: "OK", 1: "UNSUPPORTED", 2: "BAD_SHAPE", 3: "BAD_ARG", 4: "WORKSPACE
 QK_CONSISTENT, QK_NATIVE = 0, 1
 SPLIT_AUTO, SPLIT_REFERENCE, SPLIT_BALANCED, SPLIT_FINE, SPLIT_COARSE, SPLIT_NONE = range(6)
 GDN_AUTO, GDN_STEP, GDN_CHUNKED = 0, 1, 2
+ENGINE_AUTO, ENGINE_MFMA, ENGINE_VALU = 0, 1, 2
 
 EXPORTS = (
     "xq_supports_flash_attn_ext", "xq_flash_attn_ext_workspace", "xq_flash_attn_ext",
@@ -65,7 +66,8 @@ class XqFaParams(ctypes.Structure):
         ("logit_softcap", ctypes.c_float),
         ("qk_policy", ctypes.c_int32),
         ("split_mode", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 3),
+        ("engine", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
     ]
 
 
@@ -189,10 +191,11 @@ def _aligned_ptr(ws):
 # flash attention
 # ---------------------------------------------------------------------------
 
-def fa_params(scale, max_bias=0.0, softcap=0.0, qk_policy=QK_CONSISTENT, split_mode=SPLIT_AUTO):
+def fa_params(scale, max_bias=0.0, softcap=0.0, qk_policy=QK_CONSISTENT, split_mode=SPLIT_AUTO,
+              engine=ENGINE_AUTO):
     p = XqFaParams()
     p.scale, p.max_bias, p.logit_softcap = scale, max_bias, softcap
-    p.qk_policy, p.split_mode = qk_policy, split_mode
+    p.qk_policy, p.split_mode, p.engine = qk_policy, split_mode, engine
     return p
 
 
