@@ -88,10 +88,11 @@ enum xq_fa_qk_policy {
     XQ_FA_QK_NATIVE = 1,
 };
 
-/* KV split (split-K) policy. The partition depends on the KV length only, so
- * a query's result does not depend on how many queries share the call, and
- * partial states are merged in ascending split order.
- *  XQ_FA_SPLIT_AUTO: MI355X policy, about 64 splits, rows a multiple of 64.
+/* KV split (split-K) policy. The partition never depends on the number of
+ * queries, so a query's result does not depend on how many queries share the
+ * call, and partial states are merged in ascending split order.
+ *  XQ_FA_SPLIT_AUTO: MI355X policy, about 256 / (sequences x KV heads) splits
+ *    (one workgroup per CU), rows a multiple of 16.
  *  XQ_FA_SPLIT_REFERENCE: clamp(ceil(L/256), 1, 32) splits
  *    (uwp/rkva/rkva-range-profile.h:99-101).
  *  XQ_FA_SPLIT_BALANCED / FINE / COARSE: the reference's optimized modes
@@ -183,7 +184,8 @@ xq_status xq_fa_range(const float* q, const int32_t* positions, int32_t n_q, int
                       int32_t split_mode, float* out, float* lse, void* workspace,
                       size_t workspace_bytes, void* stream);
 
-/* Split count the policy picks for a KV length (host-side, pure). */
+/* Split count the policy picks for a KV length (host-side, pure; AUTO is
+ * evaluated for one sequence and one KV head). */
 int32_t xq_fa_split_count(int64_t kv_len, int32_t split_mode);
 /* Rows per split for that policy (the last split may be shorter). */
 int64_t xq_fa_split_rows(int64_t kv_len, int32_t split_mode);

@@ -80,7 +80,9 @@ int64_t opt_split_k(int64_t active, int mode) {
     return k < 1 ? 1 : k;
 }
 
-void split_policy(int64_t L, int mode, int32_t* n_splits, int64_t* rows) {
+// n_seq_heads = sequences x KV heads of the call (never the query count, so a
+// query's result does not depend on how many queries share the call).
+void split_policy(int64_t L, int mode, int64_t n_seq_heads, int32_t* n_splits, int64_t* rows) {
     if (L <= 0) {
         *n_splits = 1;
         *rows = 1;
@@ -89,9 +91,14 @@ void split_policy(int64_t L, int mode, int32_t* n_splits, int64_t* rows) {
     int64_t r = L;
     switch (mode) {
     case XQ_FA_SPLIT_AUTO: {
-        // about 64 splits of whole 64-row tiles: enough workgroups to fill 256
-        // CUs at decode shapes while the merge stays small.
-        r = cdiv(cdiv(L, 64), 64) * 64;
+        // about one workgroup per CU (256 on MI355X) over the (sequence, KV
+        // head) pairs, rows a multiple of the 16-row wave slice
+        int64_t k = cdiv(256, n_seq_heads < 1 ? 1 : n_seq_heads);
+        const int64_t kmax = cdiv(L, 16);
+        if (k > kmax) k = kmax;
+        if (k > 256) k = 256;
+        if (k < 1) k = 1;
+        r = cdiv(cdiv(L, k), 16) * 16;
         break;
     }
     case XQ_FA_SPLIT_REFERENCE: {
@@ -185,7 +192,7 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
     P.L = k->ne[1];
     P.qk_mode = (k->type == XQ_TYPE_Q8_0 || k->type == XQ_TYPE_Q4_0) ? xq::kQkInt8 : xq::kQkFloat;
     P.q_round_f16 = (p->qk_policy == XQ_FA_QK_NATIVE && k->type == XQ_TYPE_F16) ? 1 : 0;
-    split_policy(P.L, p->split_mode, &P.n_splits, &P.split_rows);
+    split_policy(P.L, p->split_mode, B * Hkv, &P.n_splits, &P.split_rows);
     if (P.n_splits > 256) return fail(XQ_ERR_UNSUPPORTED, "more than 256 KV splits");
     const int npairs = P.G * (P.NQ < 32 / P.G ? P.NQ : 32 / P.G);
     if (!xq::fa_kernel_available(P.kt, P.D, P.qk_mode, npairs))
@@ -210,14 +217,14 @@ const char* xq_last_error(void) { return g_last_error.c_str(); }
 int32_t xq_fa_split_count(int64_t kv_len, int32_t split_mode) {
     int32_t n;
     int64_t r;
-    split_policy(kv_len, split_mode, &n, &r);
+    split_policy(kv_len, split_mode, 1, &n, &r);
     return n;
 }
 
 int64_t xq_fa_split_rows(int64_t kv_len, int32_t split_mode) {
     int32_t n;
     int64_t r;
-    split_policy(kv_len, split_mode, &n, &r);
+    split_policy(kv_len, split_mode, 1, &n, &r);
     return r;
 }
 

@@ -702,10 +702,9 @@ bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Q image of the VALU engine (the matrix-core engine builds its own in LDS).
 static size_t qimg_bytes(int64_t n_rows, int d, int qk_mode, int kt) {
-    size_t b = (size_t)n_rows * qimg_words(qk_mode, kt, d) * 4;
-    const size_t m = fa_mma_qimg_bytes(n_rows, kt, d);
-    return b > m ? b : m;
+    return (size_t)n_rows * qimg_words(qk_mode, kt, d) * 4;
 }
 
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits) {
@@ -715,6 +714,16 @@ size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_spli
         bytes += align256((size_t)n_rows * n_splits * 8);
     }
     return bytes;
+}
+
+hipError_t fa_reduce_launch(const FaArgs& a, int d, hipStream_t stream) {
+    const int64_t n_rows = (int64_t)a.B * a.NQ * a.H;
+    ProfScope ps("fa_reduce", stream);
+    if (d == 128)
+        hipLaunchKernelGGL(fa_reduce<128>, dim3((uint32_t)n_rows), dim3(128), 0, stream, a);
+    else
+        hipLaunchKernelGGL(fa_reduce<256>, dim3((uint32_t)n_rows), dim3(256), 0, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
@@ -781,10 +790,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
 
     const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G);
     if (L.engine == XQ_FA_ENGINE_MFMA && !mma) return hipErrorInvalidValue;
-    if (mma) {
-        hipError_t e = fa_mma_launch(a, L, (uint8_t*)qimg, stream);
-        if (e != hipSuccess) return e;
-    } else {
+    if (mma) return fa_mma_launch(a, L, stream);
     Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);
     QprepFn qp = D == 128 ? qprep_d<128>(kt, L.qk_mode) : qprep_d<256>(kt, L.qk_mode);
     if (!p1 || !qp) return hipErrorInvalidValue;
@@ -798,14 +804,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
         ProfScope ps("fa_pass1", stream);
         hipLaunchKernelGGL(p1, dim3(n_wg), dim3(kThreads), 0, stream, a, (const uint32_t*)qimg);
     }
-    }
-    if (L.n_splits > 1) {
-        ProfScope ps("fa_reduce", stream);
-        if (D == 128)
-            hipLaunchKernelGGL(fa_reduce<128>, dim3((uint32_t)n_rows), dim3(128), 0, stream, a);
-        else
-            hipLaunchKernelGGL(fa_reduce<256>, dim3((uint32_t)n_rows), dim3(256), 0, stream, a);
-    }
+    if (L.n_splits > 1) return fa_reduce_launch(a, D, stream);
     return hipGetLastError();
 }
 

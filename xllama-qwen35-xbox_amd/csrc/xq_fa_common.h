@@ -50,6 +50,13 @@ struct FaArgs {
     float scale, softcap, max_bias, m0, m1;
     int32_t n_head_log2;
     int32_t poison;
+    // matrix-core engine: f32 Q rows (quantised inside the kernel), hi-only
+    // f16 Q for the NATIVE policy, split merge inside the kernel
+    const uint8_t* q;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int32_t hi_only;
+    int32_t fused_merge;
+    int32_t mask_vec;  // mask rows readable as 8-byte groups at every slice start
 };
 
 XQ_DEV float alibi_slope(const FaArgs& a, int h) {
@@ -88,6 +95,8 @@ XQ_DEV uint32_t lds_u16(const uint8_t* p) { return *(const uint16_t*)p; }
 
 
 struct FaLaunch;
-hipError_t fa_mma_launch(const FaArgs& a, const FaLaunch& L, uint8_t* qimg, hipStream_t stream);
+hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream);
+// Separate split-merge kernel (used when the merge cannot run inside pass 1).
+hipError_t fa_reduce_launch(const FaArgs& a, int d, hipStream_t stream);
 
 }  // namespace xq

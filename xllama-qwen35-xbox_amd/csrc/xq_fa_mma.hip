@@ -1,207 +1,179 @@
-// xq_fa_mma.hip — FLASH_ATTN_EXT pass 1 on the gfx950 matrix cores.
+// xq_fa_mma.hip — FLASH_ATTN_EXT decode / short multi-query verify on the
+// gfx950 matrix cores, one kernel launch per call: Q quantisation, the KV
+// stream, the merge of the wave states and the merge of the KV splits all
+// happen inside it.
 //
-// Same work decomposition and outputs as the VALU pass 1 in xq_fa.hip (one
-// workgroup per (sequence, KV head, query tile, KV split), 64-row tiles,
-// partial (acc, m, l) per split or the final output for one split) with both
-// products on MFMA:
-//   scores  q8_0 / q4_0 K: v_mfma_i32_16x16x32_i8 per 32-element block, i.e.
-//           the exact integer block dot of ggml's vec_dot_q8_0_q8_0 /
-//           vec_dot_q4_0_q8_0 between the q8_0-quantised Q row and the K
-//           block (q4_0 nibbles enter unsigned; 8*sum(q) is subtracted in
-//           integers), then scaled by d_k*d_q in f32;
-//           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exactly-converted K
-//           with Q split into f16 hi + lo parts (f32 Q to ~22 bits; the
-//           NATIVE policy uses the f16-rounded Q alone);
-//   values  v_mfma_f32_16x16x32_f16 with V exactly converted to f16 (int8 /
-//           nibble values via the 0x6400 exponent trick, E5M2 by a byte
-//           shift) and the softmax weights times the block scale rounded to
-//           f16 as the other operand; f32 accumulation.
-// The M dimension of both products is the (query, head) pair index (16 per
-// MFMA tile, up to two tiles); N is 16 KV rows (scores, one wave per 16 rows)
-// or 16 head dims (values, each wave a quarter of the head). K/V tiles move
-// HBM -> LDS with global_load_lds (16-byte or 4-byte per lane), double
-// buffered so the next tile streams in while the current one is computed.
-// Online softmax: per-pair maxima and sums over each wave's 16 rows by DPP
-// inside 16-lane rows, combined across the four waves through LDS in a fixed
-// order.
+// Work decomposition. A workgroup owns one (sequence, KV head, query tile,
+// KV split). Its NW waves stream disjoint 16-row slices of the split (slice j
+// goes to wave j % NW) through private double-buffered LDS rings filled by
+// global_load_lds, each with its own online softmax and no workgroup barrier
+// in the row loop. The wave states are merged through LDS at the end. With
+// several splits each workgroup writes a partial state (unnormalised output,
+// running maximum, running sum) and the last workgroup of its (sequence, KV
+// head, query tile) group to arrive merges every split in ascending split
+// order; arrivals are counted in a device array that each completed group
+// returns to zero (atomicInc wrap-around).
+//
+// Products (M x N x K of each MFMA):
+//   scores  S = K Q^T, A = 16 KV rows, B = 16 (query, head) pairs.
+//           q8_0 / q4_0 K: v_mfma_i32_16x16x32_i8 per 32-element block, the
+//           exact integer block dot of ggml's vec_dot_q8_0_q8_0 /
+//           vec_dot_q4_0_q8_0 between the K block and the q8_0-quantised Q
+//           row (q4_0 nibbles enter unsigned and 8*sum(q) is removed), then
+//           scaled by d_q and d_k in f32.
+//           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exact f16 K with Q
+//           split into f16 hi + lo parts (the NATIVE policy uses hi alone).
+//   values  O^T = V^T P^T through v_mfma_f32_16x16x16_f16, A = 16 head dims,
+//           B = the weights of 16 pairs over four rows per lane. The score
+//           tile's output registers (lane = pair, four consecutive rows) are
+//           exactly the B operand layout of this product, so the softmax
+//           weights never leave registers and every per-pair quantity
+//           (maximum, sum, rescale factor) is lane-local. V is gathered from
+//           LDS per (row, dim) and converted exactly (int8 and q4_0 nibbles
+//           through the 0x6400 exponent trick, E5M2 by a byte shift); the V
+//           block scale multiplies the weights in f16.
+// Online softmax in base 2 (scores pre-multiplied by log2 e) with a lazy
+// maximum: the running maximum moves only when a slice exceeds it by more
+// than 8, so accumulator rescales are rare; weights are taken relative to the
+// maximum plus 4 and so stay in (0, 16].
+#include <type_traits>
+
 #include "xq_fa_common.h"
 
 namespace xq {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
 
 constexpr bool is_quant(int kt) { return kt == XQ_TYPE_Q8_0 || kt == XQ_TYPE_Q4_0; }
 
-// Bytes of one Q image row for the matrix-core engine.
-//   q8_0 / q4_0 K: int8 q[D] (ggml quantize_row_q8_0 of the row), f32 d[D/32],
-//                  int32 sum(q)[D/32];
-//   F16 / E5M2 K:  f16 hi[D], f16 lo[D] with hi = f16(q), lo = f16(q - hi).
-constexpr int mma_qrow_bytes(int kt, int d) { return is_quant(kt) ? d + 8 * (d / kQK) : 4 * d; }
+constexpr int kSub = 16;               // KV rows per wave slice
+constexpr int kMaxGroups = 16384;      // arrival counters (sequence x KV head x query tile)
+constexpr int kFusedMergeMax = 4096;   // pairs x splits merged inside the kernel
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazyMax = 8.0f;       // base-2 headroom before the running maximum moves
+constexpr float kPOff = 4.0f;          // weights are exp2(x - max - 4), in (0, 16]
 
-template <int KT, int D>
-__global__ __launch_bounds__(64) void fa_qprep_mma(const uint8_t* __restrict__ q, int64_t nb1, int64_t nb2,
-                                                    int64_t nb3, int NQ, int H, int hi_only,
-                                                    uint8_t* __restrict__ img_out) {
-    constexpr int QRB = mma_qrow_bytes(KT, D);
-    const int64_t row = blockIdx.x;
-    const int h = (int)(row % H);
-    const int iq = (int)((row / H) % NQ);
-    const int b = (int)(row / ((int64_t)H * NQ));
-    const float* src = (const float*)(q + (int64_t)b * nb3 + (int64_t)iq * nb1 + (int64_t)h * nb2);
-    uint8_t* img = img_out + row * QRB;
-    const int lane = threadIdx.x;
-    if constexpr (is_quant(KT)) {
-        constexpr int VD = D / 64;
-        constexpr int LPB = kQK / VD;
-        float x[VD];
-        float amax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < VD; ++j) {
-            x[j] = src[lane * VD + j];
-            amax = fmaxf(amax, fabsf(x[j]));
-        }
-        amax = fmaxf(amax, dpp<0xB1>(amax));
-        amax = fmaxf(amax, dpp<0x4E>(amax));
-        amax = fmaxf(amax, dpp<0x141>(amax));
-        if constexpr (LPB == 16) amax = fmaxf(amax, dpp<0x140>(amax));
-        // ggml-cpu x86 quantize_row_q8_0: d = amax/127, id = 127/amax, round half to even
-        const float dblk = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        uint32_t packed = 0;
-        int qsum = 0;
-#pragma unroll
-        for (int j = 0; j < VD; ++j) {
-            const int qv = (int)rintf(x[j] * id);
-            packed |= (uint32_t)(uint8_t)(int8_t)qv << (8 * j);
-            qsum += qv;
-        }
-        if constexpr (VD == 4)
-            *(uint32_t*)(img + 4 * lane) = packed;
-        else
-            *(uint16_t*)(img + 2 * lane) = (uint16_t)packed;
-        float qs = (float)qsum;  // exact: |sum| <= 32*127
-        qs += dpp<0xB1>(qs);
-        qs += dpp<0x4E>(qs);
-        qs += dpp<0x141>(qs);
-        if constexpr (LPB == 16) qs += dpp<0x140>(qs);
-        const int blk = (lane * VD) / kQK;
-        if ((lane % LPB) == 0) {
-            ((float*)(img + D))[blk] = f16_bits_to_f32(f32_to_f16_bits(dblk));
-            ((int*)(img + D + 4 * (D / kQK)))[blk] = (int)qs;
-        }
-    } else {
-        uint16_t* hi = (uint16_t*)img;
-        uint16_t* lo = hi + D;
-        for (int e = lane; e < D; e += 64) {
-            const float x = src[e];
-            const uint32_t hb = f32_to_f16_bits(x);
-            hi[e] = (uint16_t)hb;
-            lo[e] = hi_only ? (uint16_t)0 : (uint16_t)f32_to_f16_bits(x - f16_bits_to_f32(hb));
-        }
-    }
-}
+// Arrival counters of the in-kernel split merge; zero at load, and every
+// completed group leaves its counter at zero again.
+__device__ uint32_t g_fa_arrivals[kMaxGroups];
+
+template <int KT, int D, int MT>
+struct DecCfg {
+    static constexpr int REC = rec_bytes(KT, D);
+    static constexpr int SLICE = kSub * REC;
+    static constexpr int CS = REC % 16 == 0 ? 16 : 4;  // bytes per lane per global_load_lds
+    static constexpr int CPS = SLICE / CS;             // chunks per slice per tensor
+    static constexpr int NIS = (CPS + 63) / 64;        // wave loads per slice per tensor
+    static constexpr int NB = D / kQK;                 // 32-element blocks per row
+    static constexpr int NPP = 16 * MT;
+    static constexpr bool QUANT = is_quant(KT);
+    static constexpr int QRB = QUANT ? D + 8 * NB : 0;      // LDS Q image row bytes (int8 path)
+    static constexpr int RING_W = 2 * 2 * SLICE;            // per wave: 2 stages x (K, V)
+    static constexpr bool NW8 = 8 * RING_W + NPP * QRB <= 144 * 1024 && !(MT == 2 && D == 256);
+    static constexpr int NW = NW8 ? 8 : 4;
+    static constexpr int RING = NW * RING_W;
+    static constexpr int MERGE = NW * 16 * D * 4;
+    static constexpr int SMEM = RING + NPP * QRB > MERGE ? RING + NPP * QRB : MERGE;
+    static constexpr bool FITS = SMEM + 2 * NW * NPP * 4 + 64 <= 160 * 1024;
+};
 
 // 8 K bytes (elements 8g..8g+7 of block b) of a q8_0 / q4_0 record in LDS as
-// the int8 B operand of v_mfma_i32_16x16x32_i8. q4_0 gives unsigned nibbles.
+// an int8 MFMA operand. q4_0 gives unsigned nibbles: elements 0..15 are the
+// low nibbles of bytes 0..15, elements 16..31 the high nibbles.
 template <int KT>
 XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     constexpr int BB = KT == XQ_TYPE_Q8_0 ? 34 : 18;
     const int off = KT == XQ_TYPE_Q8_0 ? BB * b + 2 + 8 * g : BB * b + 2 + 8 * (g & 1);
-    const int sh = (BB * b + 2) & 3;  // 0 or 2 for every g: depends on b only
+    const int sh = (BB * b + 2) & 3;  // 0 or 2, depends on b only
     uint32_t w0, w1;
     if (sh == 0) {
         w0 = lds_u32(rec + off);
         w1 = lds_u32(rec + off + 4);
     } else {
-        const uint32_t a = lds_u32(rec + off - 2), m = lds_u32(rec + off + 2), c = lds_u32(rec + off + 6);
-        w0 = __builtin_amdgcn_alignbyte(m, a, 2);
+        const uint32_t x = lds_u32(rec + off - 2), m = lds_u32(rec + off + 2), c = lds_u32(rec + off + 6);
+        w0 = __builtin_amdgcn_alignbyte(m, x, 2);
         w1 = __builtin_amdgcn_alignbyte(c, m, 2);
     }
     if constexpr (KT == XQ_TYPE_Q4_0) {
-        const int ns = (g >> 1) * 4;  // lane groups 2, 3 take the high nibbles
+        const int ns = (g >> 1) * 4;
         w0 = (w0 >> ns) & 0x0f0f0f0fu;
         w1 = (w1 >> ns) & 0x0f0f0f0fu;
     }
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
 
-// Four f16x2 words: rows (2e, 2e+1) of one V dim column, for e = 0..3, from
-// the two "dim pair" words X[e] = rowpair bytes. Exact conversions.
-template <int KT>
-XQ_DEV void v_pairs_to_f16(const uint32_t (&X)[4], int t, uint32_t (&out)[4]) {
-    if constexpr (KT == XQ_TYPE_Q8_0 || KT == XQ_TYPE_Q4_0) {
-        // q8_0: byte u = q ^ 0x80 gives f16(0x6400 | u) = 1024 + q + 128;
-        // q4_0: byte u = nibble gives 1024 + nibble; subtract 1152 / 1032.
-        const uint32_t sel = t == 0 ? 0x04020400u : 0x04030401u;
-        const _Float16 bias = KT == XQ_TYPE_Q8_0 ? (_Float16)-1152.0f : (_Float16)-1032.0f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t w = __builtin_amdgcn_perm(0x64646464u, X[e], sel);
-            h2 v = __builtin_bit_cast(h2, w);
-            v = v + h2{bias, bias};
-            out[e] = __builtin_bit_cast(uint32_t, v);
-        }
-    } else if constexpr (KT == XQ_TYPE_E5M2) {
-        const uint32_t sel = t == 0 ? 0x020c000cu : 0x030c010cu;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) out[e] = __builtin_amdgcn_perm(X[e], X[e], sel);
-    }
+// f16 pair (signed byte t of a, signed byte t of b), exact: v_perm places the
+// two bytes in the low bytes of the two halves (high bytes zero); one XOR
+// flips the sign bit and sets the 0x64 exponent byte, giving f16 1152 + q;
+// a packed add of -1152 leaves q.
+template <int T>
+XQ_DEV uint32_t i8x2_f16(uint32_t a, uint32_t b) {
+    const uint32_t y = __builtin_amdgcn_perm(b, a, T == 0 ? 0x0c040c00u : 0x0c050c01u) ^ 0x64806480u;
+    const h2 v = __builtin_bit_cast(h2, y) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
-// HBM -> LDS without registers: lane l's CS bytes land at lds + l*CS
-// (global_load_lds_dwordx4 / _dword). lds must be wave-uniform.
+// Reductions over the four 16-lane rows (lanes l, l^16, l^32, l^48) by
+// permlane swaps; every lane gets the same bits ((r0 op r2) op (r1 op r3)).
+XQ_DEV float xrow_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+XQ_DEV float xrow_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
+// HBM -> LDS without registers: lane l's CS bytes land at lds + l*CS.
 template <int CS>
 XQ_DEV void lds_dma(const uint8_t* g, uint8_t* lds) {
-    // the size operand must be a literal (the builtin rejects dependent values)
     if constexpr (CS == 16)
         __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
     else
         __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
-// Each wave streams its own 16-row slices of the split (slice j of the split
-// goes to wave j % 4) through a private double-buffered LDS region, with a
-// private online softmax; the four wave states are merged once at the end in
-// wave order. No workgroup barrier inside the row loop.
-template <int KT, int D, int MT>
-__global__ __launch_bounds__(kThreads) void fa_mma_pass1(FaArgs a, const uint8_t* __restrict__ qimg,
-                                                          int hi_only) {
-    constexpr int SUB = 16;                          // rows per wave slice
-    constexpr int REC = rec_bytes(KT, D);
-    constexpr int CS = REC % 16 == 0 ? 16 : 4;       // bytes per lane per global_load_lds
-    constexpr int CPS = SUB * REC / CS;              // chunks per slice per tensor
-    constexpr int NIS = (CPS + 63) / 64;             // wave loads per slice per tensor
-    constexpr int NB = D / kQK;                      // 32-element blocks per row
-    constexpr int QRB = mma_qrow_bytes(KT, D);
-    constexpr int NPP = 16 * MT;
-    constexpr bool QUANT = is_quant(KT);
-    constexpr int SPS = SUB + 4;                     // weight transpose stride (conflict-free)
-    constexpr int SLICE = SUB * REC;
+// Head dim held by accumulator register i of value tile (block c, half t) in
+// lane group lg. q8_0 / F16 / E5M2 tiles take dims 32c + 2n + t (n = tile
+// row), q4_0 tiles dims 32c + 16t + n (low / high nibbles of byte n).
+template <int KT>
+XQ_DEV int acc_dim(int c, int t, int lg, int i) {
+    return KT == XQ_TYPE_Q4_0 ? 32 * c + 16 * t + 4 * lg + i : 32 * c + 8 * lg + 2 * i + t;
+}
 
-    // per wave: K/V double buffers, weight transpose, V block scales. The K/V
-    // region doubles as the buffer of the final wave merge (2 waves x pairs x D).
-    constexpr int KV_BYTES = 4 * 2 * 2 * SLICE;
-    constexpr int MERGE_BYTES = 2 * NPP * D * 4;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[KV_BYTES > MERGE_BYTES ? KV_BYTES : MERGE_BYTES];
-    typedef uint8_t SliceBuf[2][2][SLICE];
-    SliceBuf* sKV = (SliceBuf*)smem;
-    __shared__ __attribute__((aligned(16))) float sPw[4][NPP * SPS];
-    __shared__ __attribute__((aligned(16))) float sDv[4][QUANT ? NB * SUB : 4];
-    __shared__ __attribute__((aligned(16))) float sQd[QUANT ? NB * NPP : 4];  // d_q [blk][pair]
-    __shared__ __attribute__((aligned(16))) int sQs[QUANT ? NB * NPP : 4];    // sum q [blk][pair]
-    __shared__ float sML[2][NPP][2];
+template <int KT, int D, int MT>
+__global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a) {
+    using C = DecCfg<KT, D, MT>;
+    constexpr int REC = C::REC, SLICE = C::SLICE, CS = C::CS, CPS = C::CPS, NIS = C::NIS;
+    constexpr int NB = C::NB, NPP = C::NPP, NW = C::NW, QRB = C::QRB;
+    constexpr bool QUANT = C::QUANT;
+    constexpr int BB = KT == XQ_TYPE_Q8_0 ? 34 : 18;
+    constexpr int NT = 64 * NW;
+    constexpr uint32_t kNegInfH2 = 0xfc00fc00u;  // f16 pair (-inf, -inf)
+
+    __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
+    __shared__ float sM[NW][NPP], sL[NW][NPP];
+    __shared__ int sLast;
 
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     uint32_t wg = xcd_remap(blockIdx.x, n_wg);
+    // logical order: query tile fastest, then KV head, split, sequence, so the
+    // heads reading the same rows are neighbours on one XCD (shared L2)
     const int qt = wg % a.n_qtiles;
     wg /= a.n_qtiles;
-    const int split = wg % a.n_splits;
-    wg /= a.n_splits;
     const int g_kv = wg % a.Hkv;
-    const int b = wg / a.Hkv;
+    wg /= a.Hkv;
+    const int split = wg % a.n_splits;
+    const int b = wg / a.n_splits;
     const int iq0 = qt * a.QT;
     const int nqt = min(a.QT, a.NQ - iq0);
     const int npa = nqt * a.G;
@@ -211,122 +183,232 @@ __global__ __launch_bounds__(kThreads) void fa_mma_pass1(FaArgs a, const uint8_t
     const int lr = lane & 15;
     const int lg = lane >> 4;
 
+    // ---- rows of this split; with positions each pair sees rows < its causal limit
     const int64_t r0 = (int64_t)split * a.split_rows;
     int64_t r_end = min(a.L, r0 + a.split_rows);
+    int64_t r_all = r_end;  // rows below every valid pair's limit
     if (a.positions) {
-        int64_t lim_max = 0;
+        int64_t lmax = 0, lmin = a.L;
         for (int qq = 0; qq < nqt; ++qq) {
             const int32_t pos = a.positions[iq0 + qq];
-            const int64_t causal = pos < a.origin ? 0 : (int64_t)pos - a.origin + 1;
-            lim_max = max(lim_max, min(a.L, causal));
+            const int64_t lim = min(a.L, pos < a.origin ? (int64_t)0 : (int64_t)pos - a.origin + 1);
+            lmax = max(lmax, lim);
+            lmin = min(lmin, lim);
         }
-        r_end = min(r_end, lim_max);
+        r_end = min(r_end, lmax);
+        r_all = min(r_end, lmin);
     }
     const uint8_t* kb = a.k + (int64_t)(b / a.rk3) * a.k_nb3 + (int64_t)g_kv * a.k_nb2;
     const uint8_t* vb = a.v + (int64_t)(b / a.rv3) * a.v_nb3 + (int64_t)g_kv * a.v_nb2;
-    const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
 
-    // ---- per-pair state for this lane's MFMA rows (pairs 16m + 4lg + i)
-    float m_run[MT][4], l_run[MT][4];
-    int64_t lim[MT][4];
-    const uint16_t* mrow[MT][4];
-    float slope[MT][4];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            m_run[m][i] = -INFINITY;
-            l_run[m][i] = 0.0f;
-            const int p = 16 * m + 4 * lg + i;
-            lim[m][i] = -1;  // padding pair: never valid
-            mrow[m][i] = nullptr;
-            slope[m][i] = 0.0f;
-            if (p < npa) {
-                const int qq = p / a.G, h = g_kv * a.G + p % a.G;
-                lim[m][i] = a.L;
-                if (a.positions) {
-                    const int32_t pos = a.positions[iq0 + qq];
-                    const int64_t causal = pos < a.origin ? 0 : (int64_t)pos - a.origin + 1;
-                    lim[m][i] = min(a.L, causal);
-                }
-                if (a.mask) {
-                    mrow[m][i] = (const uint16_t*)(a.mask + (int64_t)(iq0 + qq) * a.m_nb1 +
-                                                   (int64_t)(h % a.m_ne2) * a.m_nb2 + (int64_t)(b % a.m_ne3) * a.m_nb3);
-                    slope[m][i] = alibi_slope(a, h);
-                }
-            }
-        }
-
-    // ---- Q operands (A of the score MFMA): pair 16m + lr, elements 8lg..8lg+7 of each block
-    auto img_of = [&](int p) -> const uint8_t* {
-        const int qq = p / a.G, h = g_kv * a.G + p % a.G;
-        return qimg + ((int64_t)(b * a.NQ + iq0 + qq) * a.H + h) * QRB;
-    };
-    int64_t qa[QUANT ? MT : 1][QUANT ? NB : 1];
-    h8 qh[QUANT ? 1 : MT][QUANT ? 1 : NB], ql[QUANT ? 1 : MT][QUANT ? 1 : NB];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        const int p = 16 * m + lr;
-        const bool ok = p < npa;
-        const uint8_t* im = ok ? img_of(p) : qimg;
-#pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            if constexpr (QUANT) {
-                qa[m][c] = ok ? *(const int64_t*)(im + 32 * c + 8 * lg) : 0;
-            } else {
-                const h8 z = {0, 0, 0, 0, 0, 0, 0, 0};
-                qh[m][c] = ok ? *(const h8*)(im + 2 * (32 * c + 8 * lg)) : z;
-                ql[m][c] = ok ? *(const h8*)(im + 2 * D + 2 * (32 * c + 8 * lg)) : z;
-            }
-        }
-    }
-    if constexpr (QUANT) {
-        for (int e = tid; e < NB * NPP; e += kThreads) {
-            const int c = e / NPP, p = e % NPP;
-            float dq = 0.0f;
-            int sq = 0;
-            if (p < npa) {
-                const uint8_t* im = img_of(p);
-                dq = ((const float*)(im + D))[c];
-                sq = ((const int*)(im + D + 4 * NB))[c];
-            }
-            sQd[e] = dq;
-            sQs[e] = sq;
-        }
-    }
-    __syncthreads();
-
-    // ---- this wave's slices: t0 = r0 + SUB*(wave + 4*j)
-    // Chunk c = 64*i + lane of a slice is (row c / (REC/CS), byte (c % (REC/CS))*CS).
-    int64_t koff[NIS], voff[NIS];
+    // ---- per-wave ring [stage][K | V][SLICE]; chunk c = 64 i + lane of a
+    //      slice is (row c / (REC/CS), byte (c % (REC/CS)) * CS)
+    uint8_t* ring = smem + wave * C::RING_W;
+    uint32_t ko[NIS], vo[NIS];
     int crow[NIS];
 #pragma unroll
     for (int i = 0; i < NIS; ++i) {
         const int c = i * 64 + lane;
         crow[i] = c / (REC / CS);
-        koff[i] = (int64_t)crow[i] * a.k_nb1 + (c % (REC / CS)) * CS;
-        voff[i] = (int64_t)crow[i] * a.v_nb1 + (c % (REC / CS)) * CS;
+        ko[i] = (uint32_t)(crow[i] * a.k_nb1 + (c % (REC / CS)) * CS);
+        vo[i] = (uint32_t)(crow[i] * a.v_nb1 + (c % (REC / CS)) * CS);
     }
-    auto stage = [&](int64_t t0, int bf) {
-        const bool full = t0 + SUB <= r_end;
+    // one group = NIS K loads then NIS V loads (exactly 2 * NIS vector-memory
+    // instructions), then the mask loads of the slice
+    auto stage = [&](int64_t t0, int st) {
         const uint8_t* kt = kb + t0 * a.k_nb1;
         const uint8_t* vt = vb + t0 * a.v_nb1;
-        uint8_t* lk = sKV[wave][bf][0];
-        uint8_t* lv = sKV[wave][bf][1];
+        uint8_t* lk = ring + st * 2 * SLICE;
+        uint8_t* lv = lk + SLICE;
+        const bool full = t0 + kSub <= r_end;
 #pragma unroll
         for (int i = 0; i < NIS; ++i) {
-            int64_t ko = koff[i], vo = voff[i];
-            if (!full && t0 + crow[i] >= r_end) {  // rows past the split end reuse the last live row
-                const int64_t dr = t0 + crow[i] - (r_end - 1);
-                ko -= dr * a.k_nb1;
-                vo -= dr * a.v_nb1;
+            uint32_t kof = ko[i], vof = vo[i];
+            if (!full && t0 + crow[i] >= r_end) {  // rows past the end re-read the last live row
+                const uint32_t dr = (uint32_t)(t0 + crow[i] - (r_end - 1));
+                kof -= dr * (uint32_t)a.k_nb1;
+                vof -= dr * (uint32_t)a.v_nb1;
             }
-            if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) {
-                lds_dma<CS>(kt + ko, lk + i * 64 * CS);
-                lds_dma<CS>(vt + vo, lv + i * 64 * CS);
+            if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(kt + kof, lk + i * 64 * CS);
+        }
+#pragma unroll
+        for (int i = 0; i < NIS; ++i) {
+            uint32_t vof = vo[i];
+            if (!full && t0 + crow[i] >= r_end) vof -= (uint32_t)(t0 + crow[i] - (r_end - 1)) * (uint32_t)a.v_nb1;
+            if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(vt + vof, lv + i * 64 * CS);
+        }
+    };
+
+    // ---- per-pair state of this lane's pairs 16m + lr (identical in the four lane groups)
+    float m_run[MT], l_run[MT], slope2[MT];
+    int64_t lim[MT];
+    const uint16_t* mrow[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        m_run[m] = -INFINITY;
+        l_run[m] = 0.0f;
+        slope2[m] = kLog2e;
+        lim[m] = 0;  // padding pair: every row invalid
+        const int p = 16 * m + lr;
+        const bool ok = p < npa;
+        const int qq = ok ? p / a.G : 0, h = g_kv * a.G + (ok ? p % a.G : 0);
+        if (ok) {
+            lim[m] = r_end;
+            if (a.positions) {
+                const int32_t pos = a.positions[iq0 + qq];
+                lim[m] = min(r_end, pos < a.origin ? (int64_t)0 : (int64_t)pos - a.origin + 1);
+            }
+            slope2[m] = alibi_slope(a, h) * kLog2e;
+        }
+        // padding pairs read the first pair's mask row (always valid memory)
+        mrow[m] = a.mask ? (const uint16_t*)(a.mask + (int64_t)(iq0 + qq) * a.m_nb1 + (int64_t)(h % a.m_ne2) * a.m_nb2 +
+                                             (int64_t)(b % a.m_ne3) * a.m_nb3)
+                         : nullptr;
+    }
+    // additive mask of a slice as f16 pairs (rows 4lg + 0,1 and 4lg + 2,3), with
+    // -inf for rows past the pair's limit
+    auto load_mask = [&](int64_t t, uint32_t (&mk)[MT][2]) {
+        const int64_t r = t + 4 * lg;
+        if (t + kSub <= r_all) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (!a.mask) {
+                    mk[m][0] = mk[m][1] = 0;
+                } else if (a.mask_vec) {
+                    const uint2 w = *(const uint2*)(mrow[m] + r);
+                    mk[m][0] = w.x;
+                    mk[m][1] = w.y;
+                } else {
+                    mk[m][0] = (uint32_t)mrow[m][r] | ((uint32_t)mrow[m][r + 1] << 16);
+                    mk[m][1] = (uint32_t)mrow[m][r + 2] | ((uint32_t)mrow[m][r + 3] << 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = r + i < lim[m] ? (a.mask ? (uint32_t)mrow[m][r + i] : 0u) : 0xfc00u;
+                mk[m][0] = v[0] | (v[1] << 16);
+                mk[m][1] = v[2] | (v[3] << 16);
             }
         }
     };
+
+    const int64_t step = (int64_t)kSub * NW;
+    int64_t t0 = r0 + kSub * wave;
+    uint32_t mk[2][MT][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) mk[s2][m][0] = mk[s2][m][1] = kNegInfH2;
+    // both ring stages in flight before the Q image is built
+    if (t0 < r_end) {
+        stage(t0, 0);
+        load_mask(t0, mk[0]);
+    }
+    if (t0 + step < r_end) {
+        stage(t0 + step, 1);
+        load_mask(t0 + step, mk[1]);
+    }
+
+    // ---- int8 Q image of the tile's pairs in LDS (pairs >= npa are zero)
+    uint8_t* sQ = smem + C::RING;
+    if constexpr (QUANT) {
+        constexpr int VD = D / 64;
+        constexpr int LPB = kQK / VD;
+        constexpr int PPW = (NPP + NW - 1) / NW;
+        float x[PPW][VD];
+#pragma unroll
+        for (int k = 0; k < PPW; ++k) {  // every load first
+            const int p = wave + k * NW;
+            const bool ok = p < npa;
+            const float* src = (const float*)a.q;
+            if (ok) {
+                const int qq = p / a.G, h = g_kv * a.G + p % a.G;
+                src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+            }
+#pragma unroll
+            for (int j = 0; j < VD; ++j) x[k][j] = ok ? src[lane * VD + j] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < PPW; ++k) {
+            const int p = wave + k * NW;
+            if (p >= NPP) break;
+            uint8_t* img = sQ + p * QRB;
+            // ggml-cpu x86 quantize_row_q8_0: d = amax/127 (stored as f16),
+            // id = 127/amax, q = round-half-even(x * id)
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VD; ++j) amax = fmaxf(amax, fabsf(x[k][j]));
+            amax = fmaxf(amax, dpp<0xB1>(amax));
+            amax = fmaxf(amax, dpp<0x4E>(amax));
+            amax = fmaxf(amax, dpp<0x141>(amax));
+            if constexpr (LPB == 16) amax = fmaxf(amax, dpp<0x140>(amax));
+            const float dblk = amax / 127.0f;
+            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            uint32_t packed = 0;
+            int qsum = 0;
+#pragma unroll
+            for (int j = 0; j < VD; ++j) {
+                const int qv = (int)rintf(x[k][j] * id);
+                packed |= (uint32_t)(uint8_t)(int8_t)qv << (8 * j);
+                qsum += qv;
+            }
+            if constexpr (VD == 4)
+                *(uint32_t*)(img + 4 * lane) = packed;
+            else
+                *(uint16_t*)(img + 2 * lane) = (uint16_t)packed;
+            float qs = (float)qsum;  // exact: |sum| <= 32*127
+            qs += dpp<0xB1>(qs);
+            qs += dpp<0x4E>(qs);
+            qs += dpp<0x141>(qs);
+            if constexpr (LPB == 16) qs += dpp<0x140>(qs);
+            if ((lane % LPB) == 0) {
+                const int blk = (lane * VD) / kQK;
+                const float dqv = f16_bits_to_f32(f32_to_f16_bits(dblk));
+                ((float*)(img + D))[blk] = dqv;
+                // q4_0: the dot with unsigned nibbles carries +8*sum(q); removed as -8*sum*d_q
+                ((float*)(img + D + 4 * NB))[blk] = KT == XQ_TYPE_Q4_0 ? -8.0f * qs * dqv : 0.0f;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- B operands of the score product: pair 16m + lr, elements 8lg..8lg+7 of each block
+    int64_t qb[QUANT ? MT : 1][QUANT ? NB : 1];
+    float dq[QUANT ? MT : 1][QUANT ? NB : 1], qcorr[KT == XQ_TYPE_Q4_0 ? MT : 1][KT == XQ_TYPE_Q4_0 ? NB : 1];
+    h8 qh[QUANT ? 1 : MT][QUANT ? 1 : NB], ql[QUANT ? 1 : MT][QUANT ? 1 : NB];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        const int p = 16 * m + lr;
+        const uint8_t* img = sQ + p * QRB;
+        const float* src = nullptr;  // f32 Q row of the pair (float K)
+        if (!QUANT && p < npa) {
+            const int qq = p / a.G, h = g_kv * a.G + p % a.G;
+            src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            if constexpr (QUANT) {
+                qb[m][c] = *(const int64_t*)(img + 32 * c + 8 * lg);
+                dq[m][c] = ((const float*)(img + D))[c];
+                if constexpr (KT == XQ_TYPE_Q4_0) qcorr[m][c] = ((const float*)(img + D + 4 * NB))[c];
+            } else {
+                // Q = f16 hi + f16 lo (lo = 0 for the NATIVE policy); NaN as ggml's f16 conversion
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float xv = src ? src[32 * c + 8 * lg + j] : 0.0f;
+                    const uint32_t hb = f32_to_f16_bits(xv);
+                    qh[m][c][j] = __builtin_bit_cast(_Float16, (uint16_t)hb);
+                    ql[m][c][j] = a.hi_only ? (_Float16)0.0f
+                                            : __builtin_bit_cast(_Float16, (uint16_t)f32_to_f16_bits(xv - f16_bits_to_f32(hb)));
+                }
+            }
+        }
+    }
+    const float sc2 = a.scale * kLog2e;
+    const float cap2 = a.softcap * kLog2e;
 
     f4 acc[MT][2 * NB];
 #pragma unroll
@@ -334,64 +416,45 @@ __global__ __launch_bounds__(kThreads) void fa_mma_pass1(FaArgs a, const uint8_t
 #pragma unroll
         for (int n = 0; n < 2 * NB; ++n) acc[m][n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    float* pw = sPw[wave];
-    float* dvw = sDv[wave];
-    int bf = 0;
-    int64_t t0 = r0 + SUB * wave;
-    if (t0 < r_end) stage(t0, 0);
-    for (; t0 < r_end; t0 += 4 * SUB, bf ^= 1) {
-        const int64_t tn = t0 + 4 * SUB;
-        // mask values of this slice (the lane's row lr), issued before the wait
-        float mv[MT][4];
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                mv[m][i] = (mrow[m][i] && t0 + lr < r_end) ? slope[m][i] * f16_bits_to_f32(mrow[m][i][t0 + lr]) : 0.0f;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // ---- one 16-row slice from ring stage S (S static: the loop is unrolled by two)
+    auto slice = [&](int64_t t, auto stage_tag) {
+        constexpr int S = decltype(stage_tag)::value;
+        // this slice's group is complete once at most one group (the next slice's,
+        // >= 2 * NIS instructions, issued later) is outstanding; loads return in order
+        if (t + step < r_end)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
-        if (tn < r_end) stage(tn, bf ^ 1);
-        const uint8_t* K = sKV[wave][bf][0];
-        const uint8_t* V = sKV[wave][bf][1];
-        const uint8_t* krec = K + lr * REC;
+        const uint8_t* Ks = ring + S * 2 * SLICE;
+        const uint8_t* Vs = Ks + SLICE;
 
-        // ---- scores: pairs x 16 rows
+        // -- scores s[m][i]: row t + 4lg + i, pair 16m + lr
         float s[MT][4];
         if constexpr (QUANT) {
-            constexpr int BB = KT == XQ_TYPE_Q8_0 ? 34 : 18;
-            i4 I[MT][NB];
-            float dk[NB];
 #pragma unroll
-            for (int c = 0; c < NB; ++c) {
-                const int64_t kop = k_block_bytes<KT>(krec, c, lg);
-                dk[c] = f16_bits_to_f32(lds_u16(krec + BB * c));
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const i4 z = {0, 0, 0, 0};
-                    I[m][c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(qa[m][c], kop, z, 0, 0, 0);
-                }
-            }
-            // V block scales of this slice (rows 0..15), written for the value step
-#pragma unroll
-            for (int j = 0; j < NB * SUB / 64; ++j) {
-                const int e = lane + 64 * j;
-                const int c = e / SUB, r = e % SUB;
-                dvw[e] = f16_bits_to_f32(lds_u16(V + r * REC + BB * c));
-            }
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
+            for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[m][i] = 0.0f;
 #pragma unroll
-                for (int c = 0; c < NB; ++c) {
-                    const f4 dq = *(const f4*)(sQd + c * NPP + 16 * m + 4 * lg);
-                    i4 sq4 = {0, 0, 0, 0};
-                    if constexpr (KT == XQ_TYPE_Q4_0) sq4 = *(const i4*)(sQs + c * NPP + 16 * m + 4 * lg);
+            for (int c = 0; c < NB; ++c) {
+                const int64_t ka = k_block_bytes<KT>(Ks + lr * REC, c, lg);
+                uint32_t dkw[4];  // K scales of rows 4lg + i (low or high half)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dkw[i] = lds_u32(Ks + (4 * lg + i) * REC + ((BB * c) & ~3));
+                const bool dhi = ((BB * c) & 2) != 0;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const i4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qb[m][c], i4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        int ii = I[m][c][i];
-                        if constexpr (KT == XQ_TYPE_Q4_0) ii -= 8 * sq4[i];
-                        s[m][i] = fmaf((float)ii, dk[c] * dq[i], s[m][i]);
+                        float tv = (float)I[i];
+                        if constexpr (KT == XQ_TYPE_Q4_0)
+                            tv = fmaf(tv, dq[m][c], qcorr[m][c]);
+                        else
+                            tv = tv * dq[m][c];
+                        const h2 dh = __builtin_bit_cast(h2, dkw[i]);
+                        s[m][i] = fmaf(tv, dhi ? (float)dh[1] : (float)dh[0], s[m][i]);
                     }
                 }
             }
@@ -401,19 +464,19 @@ __global__ __launch_bounds__(kThreads) void fa_mma_pass1(FaArgs a, const uint8_t
             for (int m = 0; m < MT; ++m) sc[m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
-                h8 kop;
+                h8 kf;
                 if constexpr (KT == XQ_TYPE_F16) {
-                    kop = *(const h8*)(krec + 64 * c + 16 * lg);
+                    kf = *(const h8*)(Ks + lr * REC + 64 * c + 16 * lg);
                 } else {  // E5M2: byte b -> f16 bits b << 8
-                    const uint2 w = *(const uint2*)(krec + 32 * c + 8 * lg);
+                    const uint2 w = *(const uint2*)(Ks + lr * REC + 32 * c + 8 * lg);
                     const uint4 hv = {__builtin_amdgcn_perm(w.x, w.x, 0x010c000cu), __builtin_amdgcn_perm(w.x, w.x, 0x030c020cu),
                                       __builtin_amdgcn_perm(w.y, w.y, 0x010c000cu), __builtin_amdgcn_perm(w.y, w.y, 0x030c020cu)};
-                    kop = __builtin_bit_cast(h8, hv);
+                    kf = __builtin_bit_cast(h8, hv);
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
-                    sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[m][c], kop, sc[m], 0, 0, 0);
-                    if (!hi_only) sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[m][c], kop, sc[m], 0, 0, 0);
+                    sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[m][c], sc[m], 0, 0, 0);
+                    if (!a.hi_only) sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[m][c], sc[m], 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -422,251 +485,350 @@ __global__ __launch_bounds__(kThreads) void fa_mma_pass1(FaArgs a, const uint8_t
                 for (int i = 0; i < 4; ++i) s[m][i] = sc[m][i];
         }
 
-        // ---- online softmax over this slice (rows t0 + lr), per pair
-        const int64_t arow = t0 + lr;
-        bool moved = false;
-        float alpha[MT][4];
+        // -- online softmax (base 2); the mask pairs carry -inf for invalid rows
+        float x[MT][4];
+        bool grow = false;
+        float mnew[MT];
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int p = 16 * m + 4 * lg + i;
-                float x = s[m][i] * a.scale;
-                if (a.softcap != 0.0f) x = a.softcap * tanhf(x);
-                const bool valid = arow < r_end && arow < lim[m][i] && mv[m][i] != -INFINITY;
-                x = valid ? x + mv[m][i] : -INFINITY;
-                const float m_new = fmaxf(m_run[m][i], row16_max_ord(x));
-                alpha[m][i] = m_new == -INFINITY ? 1.0f : fast_exp(m_run[m][i] - m_new);
-                const float pr = x == -INFINITY ? 0.0f : fast_exp(x - m_new);
-                moved |= alpha[m][i] != 1.0f;
-                m_run[m][i] = m_new;
-                l_run[m][i] = fmaf(l_run[m][i], alpha[m][i], row16_sum(pr));
-                pw[p * SPS + lr] = pr;  // transpose through LDS: [pair][row]
+                const h2 mh = __builtin_bit_cast(h2, mk[S][m][i >> 1]);
+                const float v = a.softcap != 0.0f ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
+                x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
             }
-        if (__builtin_amdgcn_ballot_w64(moved)) {
-#pragma unroll
-            for (int m = 0; m < MT; ++m)
-#pragma unroll
-                for (int n = 0; n < 2 * NB; ++n)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[m][n][i] *= alpha[m][i];
+            const float mt = xrow_max(fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3])));
+            mnew[m] = mt > m_run[m] + kLazyMax ? mt : m_run[m];
+            grow |= mnew[m] != m_run[m];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- values: A = weights of pair 16m + lr at rows 4lg..4lg+3 (x V block scale),
-        //      B = V rows 4lg..4lg+3 at dims 32*blk + 2*lr + t
-        f4 pv[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) pv[m] = *(const f4*)(pw + (16 * m + lr) * SPS + 4 * lg);
-#pragma unroll
-        for (int blk = 0; blk < NB; ++blk) {
-            f4 d4 = f4{1.0f, 1.0f, 1.0f, 1.0f};
-            if constexpr (QUANT) d4 = *(const f4*)(dvw + blk * SUB + 4 * lg);
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            h4 A[MT];
+        if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const f4 x = pv[m] * d4;
-                A[m] = h4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
-            }
-            uint32_t T0[2], T1[2];
-            if constexpr (KT == XQ_TYPE_F16) {
+                const float al = mnew[m] == m_run[m] ? 1.0f : __builtin_amdgcn_exp2f(m_run[m] - mnew[m]);
+                l_run[m] *= al;
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t wa = lds_u32(V + (4 * lg + 2 * e) * REC + 64 * blk + 4 * lr);
-                    const uint32_t wb2 = lds_u32(V + (4 * lg + 2 * e + 1) * REC + 64 * blk + 4 * lr);
-                    T0[e] = __builtin_amdgcn_perm(wb2, wa, 0x05040100u);
-                    T1[e] = __builtin_amdgcn_perm(wb2, wa, 0x07060302u);
+                for (int n = 0; n < 2 * NB; ++n) acc[m][n] *= al;
+                m_run[m] = mnew[m];
+            }
+        }
+        h2 P[MT][2];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float mu = m_run[m] == -INFINITY ? 0.0f : m_run[m] + kPOff;
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(x[m][i] - mu);
+            l_run[m] += (p[0] + p[1]) + (p[2] + p[3]);
+            P[m][0] = h2{(_Float16)p[0], (_Float16)p[1]};
+            P[m][1] = h2{(_Float16)p[2], (_Float16)p[3]};
+        }
+
+        // -- values: acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x P^T
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            h4 Bv[MT];
+            if constexpr (QUANT) {
+                uint32_t dvw[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
+                const uint32_t sel = ((BB * c) & 2) ? 0x07060302u : 0x05040100u;
+                const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[1], dvw[0], sel));
+                const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[3], dvw[2], sel));
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const h2 u = P[m][0] * d01, w = P[m][1] * d23;
+                    Bv[m] = h4{u[0], u[1], w[0], w[1]};
                 }
             } else {
-                int off;
-                if constexpr (KT == XQ_TYPE_Q8_0) off = 34 * blk + 2 + 2 * lr;
-                else if constexpr (KT == XQ_TYPE_Q4_0) off = 18 * blk + 2 + 2 * (lr & 7);
-                else off = 32 * blk + 2 * lr;
-                uint32_t X[2];
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const uint32_t ua = lds_u16(V + (4 * lg + 2 * e) * REC + off);
-                    const uint32_t ub = lds_u16(V + (4 * lg + 2 * e + 1) * REC + off);
-                    uint32_t x = ua | (ub << 16);
-                    if constexpr (KT == XQ_TYPE_Q8_0) x ^= 0x80808080u;
-                    if constexpr (KT == XQ_TYPE_Q4_0) x = (x >> ((lr >> 3) * 4)) & 0x0f0f0f0fu;
-                    X[e] = x;
-                }
-                if constexpr (KT == XQ_TYPE_E5M2) {
+                for (int m = 0; m < MT; ++m) Bv[m] = h4{P[m][0][0], P[m][0][1], P[m][1][0], P[m][1][1]};
+            }
+            // V^T operands of tiles t = 0, 1: f16 pairs of rows (0,1), (2,3)
+            uint32_t X[4], A0[2], A1[2];
 #pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        T0[e] = __builtin_amdgcn_perm(X[e], X[e], 0x020c000cu);
-                        T1[e] = __builtin_amdgcn_perm(X[e], X[e], 0x030c010cu);
-                    }
+            for (int e = 0; e < 4; ++e) {
+                const uint8_t* vr = Vs + (4 * lg + e) * REC;
+                if constexpr (KT == XQ_TYPE_Q8_0)
+                    X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
+                else if constexpr (KT == XQ_TYPE_Q4_0)
+                    X[e] = *(const uint8_t*)(vr + 18 * c + 2 + lr);
+                else if constexpr (KT == XQ_TYPE_F16)
+                    X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
+                else
+                    X[e] = lds_u16(vr + 32 * c + 2 * lr);
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t x0 = X[2 * e], x1 = X[2 * e + 1];
+                if constexpr (KT == XQ_TYPE_Q8_0) {
+                    A0[e] = i8x2_f16<0>(x0, x1);
+                    A1[e] = i8x2_f16<1>(x0, x1);
+                } else if constexpr (KT == XQ_TYPE_Q4_0) {
+                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+                    const uint32_t w = x0 | (x1 << 16);
+                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
+                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
+                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
+                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
+                } else if constexpr (KT == XQ_TYPE_F16) {
+                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
                 } else {
-                    const _Float16 bias = KT == XQ_TYPE_Q8_0 ? (_Float16)-1152.0f : (_Float16)-1032.0f;
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        h2 v0 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, X[e], 0x04020400u));
-                        h2 v1 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, X[e], 0x04030401u));
-                        v0 = v0 + h2{bias, bias};
-                        v1 = v1 + h2{bias, bias};
-                        T0[e] = __builtin_bit_cast(uint32_t, v0);
-                        T1[e] = __builtin_bit_cast(uint32_t, v1);
-                    }
+                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x040c000cu);
+                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x050c010cu);
                 }
             }
-            typedef _Float16 h4t __attribute__((ext_vector_type(4)));
-            const h4t B0 = __builtin_bit_cast(h4t, uint2{T0[0], T0[1]});
-            const h4t B1 = __builtin_bit_cast(h4t, uint2{T1[0], T1[1]});
+            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
+            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                acc[m][2 * blk] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[m], B0, acc[m][2 * blk], 0, 0, 0);
-                acc[m][2 * blk + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(A[m], B1, acc[m][2 * blk + 1], 0, 0, 0);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
             }
         }
-        __builtin_amdgcn_wave_barrier();  // pw / dvw reads done before the next slice writes them
+
+        // -- refill this stage with the slice two steps ahead
+        const int64_t tr = t + 2 * step;
+        if (tr < r_end) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage done
+            stage(tr, S);
+            load_mask(tr, mk[S]);
+        }
+    };
+    for (; t0 < r_end; t0 += 2 * step) {
+        slice(t0, std::integral_constant<int, 0>{});
+        if (t0 + step < r_end) slice(t0 + step, std::integral_constant<int, 1>{});
     }
 
-    // ---- merge the wave states: (w0 + w2) + (w1 + w3), a fixed order. Partner
-    //      wave states go through LDS in the MFMA layout of the accumulators.
-    float* mo = (float*)smem;  // [2][NPP][D]
-    auto publish = [&](int slot) {
+    // ---- merge the wave states per 16-pair group through LDS (fixed wave order)
+    const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
+    __syncthreads();  // every wave is done with its ring and the Q image
+    float* mb = (float*)smem;  // [NW][16][D]
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+    for (int m = 0; m < MT; ++m) {
+        const float lt = xrow_sum(l_run[m]);
+        if (lg == 0) {
+            sM[wave][16 * m + lr] = m_run[m] == -INFINITY ? -INFINITY : m_run[m] + kPOff;
+            sL[wave][16 * m + lr] = lt;
+        }
+        float* mw = mb + (wave * 16 + lr) * D;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = 16 * m + 4 * lg + i;
-                if (lr == 0) {
-                    sML[slot][p][0] = m_run[m][i];
-                    sML[slot][p][1] = l_run[m][i];
-                }
+        for (int c = 0; c < NB; ++c)
 #pragma unroll
-                for (int blk = 0; blk < NB; ++blk)
-                    *(float2*)(mo + (slot * NPP + p) * D + 32 * blk + 2 * lr) =
-                        make_float2(acc[m][2 * blk][i], acc[m][2 * blk + 1][i]);
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mw[acc_dim<KT>(c, t, lg, i)] = acc[m][2 * c + t][i];
+        __syncthreads();
+        for (int e = tid; e < 16 * (D / 4); e += NT) {
+            const int pl = e / (D / 4), d4 = e % (D / 4);
+            const int p = 16 * m + pl;
+            if (p >= npa) continue;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) M = fmaxf(M, sM[w][p]);
+            float Ls = 0.0f;
+            f4 o = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float mw_ = sM[w][p];
+                const float ew = mw_ == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
+                Ls = fmaf(sL[w][p], ew, Ls);
+                o += ew * *(const f4*)(mb + (w * 16 + pl) * D + 4 * d4);
             }
-    };
-    auto absorb = [&](int slot) {
+            const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
+            const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
+            const float Mn = M == -INFINITY ? -INFINITY : M * kLn2;  // natural-log units
+            if (a.n_splits == 1) {
+                float a1, inv, lse;
+                fa_finalize(Ls == 0.0f ? -INFINITY : Mn, Ls, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
+                float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
+                *(f4*)(od + 4 * d4) = (o * a1) * inv;
+                if (d4 == 0 && a.lse) a.lse[row] = lse;
+            } else if (a.fused_merge) {
+                // agent-scope stores: visible to the merging workgroup on any XCD
+                // once acknowledged, with no L2 writeback
+                float* po = a.part_o + (row * a.n_splits + split) * D + 4 * d4;
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = 16 * m + 4 * lg + i;
-                const float mp = sML[slot][p][0], lp = sML[slot][p][1];
-                const float M = fmaxf(m_run[m][i], mp);
-                const float fo = M == -INFINITY ? 0.0f : fast_exp(m_run[m][i] - M);
-                const float fp = M == -INFINITY ? 0.0f : fast_exp(mp - M);
-                l_run[m][i] = fmaf(l_run[m][i], fo, lp * fp);
-                m_run[m][i] = M;
-#pragma unroll
-                for (int blk = 0; blk < NB; ++blk) {
-                    const float2 o = *(const float2*)(mo + (slot * NPP + p) * D + 32 * blk + 2 * lr);
-                    acc[m][2 * blk][i] = fmaf(acc[m][2 * blk][i], fo, o.x * fp);
-                    acc[m][2 * blk + 1][i] = fmaf(acc[m][2 * blk + 1][i], fo, o.y * fp);
+                for (int j = 0; j < 4; ++j) __hip_atomic_store(po + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d4 == 0) {
+                    float* pm = (float*)(a.part_ml + row * a.n_splits + split);
+                    __hip_atomic_store(pm, Mn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(pm + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+            } else {
+                *(f4*)(a.part_o + (row * a.n_splits + split) * D + 4 * d4) = o;
+                if (d4 == 0) a.part_ml[row * a.n_splits + split] = make_float2(Mn, Ls);
             }
-    };
-    __syncthreads();  // every wave's slices done: the K/V region is free
-    if (wave >= 2) publish(wave - 2);
+        }
+        __syncthreads();
+    }
+    if (a.n_splits == 1 || !a.fused_merge) return;
+
+    // ---- the last workgroup of the group merges every split (ascending split order).
+    //      The partial stores above are acknowledged (vmcnt 0) before the arrival is
+    //      counted; the merging workgroup reads them with agent-scope loads.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (wave < 2) absorb(wave);
+    if (tid == 0) {
+        const uint32_t gidx = ((uint32_t)b * a.Hkv + g_kv) * a.n_qtiles + qt;
+        sLast = __builtin_amdgcn_atomic_inc32(&g_fa_arrivals[gidx], (uint32_t)(a.n_splits - 1), __ATOMIC_RELAXED, "agent") ==
+                (uint32_t)(a.n_splits - 1);
+    }
     __syncthreads();
-    if (wave == 1) publish(0);
+    if (!sLast) return;
+    const int S = a.n_splits;
+    int* sbad = (int*)smem;  // [npa]: a participating state or a numerator is non-finite
+    for (int p = tid; p < npa; p += NT) sbad[p] = 0;
     __syncthreads();
-    if (wave == 0) {
-        absorb(0);
+    // item = (pair, 4 dims); each thread merges its items' splits in ascending order
+    constexpr int MAXIT = (NPP * (D / 4) + NT - 1) / NT;
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int p = 16 * m + 4 * lg + i;
-                if (p >= npa) continue;
-                const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
-                const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
-                if (a.n_splits == 1) {
-                    float a1, inv, l;
-                    fa_finalize(m_run[m][i], l_run[m][i], a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, l);
-                    float* o = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
-#pragma unroll
-                    for (int blk = 0; blk < NB; ++blk)
-                        *(float2*)(o + 32 * blk + 2 * lr) = make_float2((acc[m][2 * blk][i] * a1) * inv,
-                                                                         (acc[m][2 * blk + 1][i] * a1) * inv);
-                    if (lr == 0 && a.lse) a.lse[row] = l;
-                } else {
-                    float* o = a.part_o + (row * a.n_splits + split) * D;
-#pragma unroll
-                    for (int blk = 0; blk < NB; ++blk)
-                        *(float2*)(o + 32 * blk + 2 * lr) = make_float2(acc[m][2 * blk][i], acc[m][2 * blk + 1][i]);
-                    if (lr == 0) a.part_ml[row * a.n_splits + split] = make_float2(m_run[m][i], l_run[m][i]);
-                }
+    for (int it = 0; it < MAXIT; ++it) {
+        const int e = tid + it * NT;
+        if (e >= npa * (D / 4)) continue;
+        const int p = e / (D / 4), d4 = e % (D / 4);
+        const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
+        const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
+        const float* pml = (const float*)(a.part_ml + row * S);
+        const float* po = a.part_o + row * S * D + 4 * d4;
+        float M = -3.402823466e38f;
+        int bad = 0;
+        for (int s0 = 0; s0 < S; ++s0) {
+            const float mv = __hip_atomic_load(pml + 2 * s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float lv = __hip_atomic_load(pml + 2 * s0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lv != 0.0f) {
+                if (!isfinite(lv) || lv < 0.0f || !isfinite(mv))
+                    bad = 1;
+                else
+                    M = fmaxf(M, mv);
             }
+        }
+        float Ls = 0.0f;
+        f4 o = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int s0 = 0; s0 < S; ++s0) {
+            const float mv = __hip_atomic_load(pml + 2 * s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float lv = __hip_atomic_load(pml + 2 * s0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            f4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                v[j] = __hip_atomic_load(po + (int64_t)s0 * D + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lv != 0.0f) {
+                const float w = expf(mv - M);
+                Ls = fmaf(lv, w, Ls);
+                o += v * w;
+            }
+        }
+        int badl = bad || !isfinite(Ls);
+        float a1, inv, lse;
+        fa_finalize(Ls == 0.0f ? -INFINITY : M, Ls, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
+        if (!isfinite(inv) || (Ls != 0.0f && !isfinite(lse))) badl = 1;
+        o = (o * a1) * inv;
+        if (a.poison && (badl || !(isfinite(o[0]) && isfinite(o[1]) && isfinite(o[2]) && isfinite(o[3]))))
+            atomicOr(&sbad[p], 1);
+        float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
+        *(f4*)(od + 4 * d4) = o;
+        if (d4 == 0 && a.lse) a.lse[row] = lse;
+    }
+    if (!a.poison) return;
+    __syncthreads();
+    // poison: any non-finite participating state or numerator makes the whole row NaN
+#pragma unroll
+    for (int it = 0; it < MAXIT; ++it) {
+        const int e = tid + it * NT;
+        if (e >= npa * (D / 4)) continue;
+        const int p = e / (D / 4), d4 = e % (D / 4);
+        if (!sbad[p]) continue;
+        const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
+        float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
+        *(f4*)(od + 4 * d4) = f4{NAN, NAN, NAN, NAN};
+        if (d4 == 0 && a.lse) a.lse[(int64_t)b * rows_per_seq + (int64_t)iq * a.H + h] = NAN;
     }
 }
 
 // ---------------------------------------------------------------- dispatch
 
-using MmaPass1Fn = void (*)(FaArgs, const uint8_t*, int);
-using MmaQprepFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, int, int, uint8_t*);
+using DecFn = void (*)(FaArgs);
 
-template <int KT, int D>
-static MmaPass1Fn mma_for(int mt) {
-    return mt == 1 ? fa_mma_pass1<KT, D, 1> : mt == 2 ? fa_mma_pass1<KT, D, 2> : nullptr;
+template <int KT, int D, int MT>
+static DecFn dec_inst() {
+    if constexpr (DecCfg<KT, D, MT>::FITS)
+        return fa_dec<KT, D, MT>;
+    else
+        return nullptr;
 }
 
-static MmaPass1Fn mma_lookup(int kt, int d, int mt) {
+template <int KT, int D>
+static DecFn dec_for(int mt) {
+    return mt == 1 ? dec_inst<KT, D, 1>() : mt == 2 ? dec_inst<KT, D, 2>() : nullptr;
+}
+
+template <int KT, int D>
+static int waves_for(int mt) {
+    return mt == 1 ? DecCfg<KT, D, 1>::NW : DecCfg<KT, D, 2>::NW;
+}
+
+static DecFn dec_lookup(int kt, int d, int mt, int* waves) {
     if (d == 128) {
         switch (kt) {
-        case XQ_TYPE_Q8_0: return mma_for<XQ_TYPE_Q8_0, 128>(mt);
-        case XQ_TYPE_Q4_0: return mma_for<XQ_TYPE_Q4_0, 128>(mt);
-        case XQ_TYPE_F16: return mma_for<XQ_TYPE_F16, 128>(mt);
-        case XQ_TYPE_E5M2: return mma_for<XQ_TYPE_E5M2, 128>(mt);
+        case XQ_TYPE_Q8_0: *waves = waves_for<XQ_TYPE_Q8_0, 128>(mt); return dec_for<XQ_TYPE_Q8_0, 128>(mt);
+        case XQ_TYPE_Q4_0: *waves = waves_for<XQ_TYPE_Q4_0, 128>(mt); return dec_for<XQ_TYPE_Q4_0, 128>(mt);
+        case XQ_TYPE_F16: *waves = waves_for<XQ_TYPE_F16, 128>(mt); return dec_for<XQ_TYPE_F16, 128>(mt);
+        case XQ_TYPE_E5M2: *waves = waves_for<XQ_TYPE_E5M2, 128>(mt); return dec_for<XQ_TYPE_E5M2, 128>(mt);
         }
     } else if (d == 256) {
         switch (kt) {
-        case XQ_TYPE_Q8_0: return mma_for<XQ_TYPE_Q8_0, 256>(mt);
-        case XQ_TYPE_Q4_0: return mma_for<XQ_TYPE_Q4_0, 256>(mt);
-        case XQ_TYPE_F16: return mma_for<XQ_TYPE_F16, 256>(mt);
-        case XQ_TYPE_E5M2: return mma_for<XQ_TYPE_E5M2, 256>(mt);
+        case XQ_TYPE_Q8_0: *waves = waves_for<XQ_TYPE_Q8_0, 256>(mt); return dec_for<XQ_TYPE_Q8_0, 256>(mt);
+        case XQ_TYPE_Q4_0: *waves = waves_for<XQ_TYPE_Q4_0, 256>(mt); return dec_for<XQ_TYPE_Q4_0, 256>(mt);
+        case XQ_TYPE_F16: *waves = waves_for<XQ_TYPE_F16, 256>(mt); return dec_for<XQ_TYPE_F16, 256>(mt);
+        case XQ_TYPE_E5M2: *waves = waves_for<XQ_TYPE_E5M2, 256>(mt); return dec_for<XQ_TYPE_E5M2, 256>(mt);
         }
     }
     return nullptr;
 }
 
-static MmaQprepFn mma_qprep_lookup(int kt, int d) {
-    if (d == 128) {
-        if (is_quant(kt)) return kt == XQ_TYPE_Q8_0 ? fa_qprep_mma<XQ_TYPE_Q8_0, 128> : fa_qprep_mma<XQ_TYPE_Q4_0, 128>;
-        return fa_qprep_mma<XQ_TYPE_F16, 128>;
-    }
-    if (is_quant(kt)) return kt == XQ_TYPE_Q8_0 ? fa_qprep_mma<XQ_TYPE_Q8_0, 256> : fa_qprep_mma<XQ_TYPE_Q4_0, 256>;
-    return fa_qprep_mma<XQ_TYPE_F16, 256>;
-}
-
 bool fa_mma_available(int kt, int d, int qk_mode, int n_pairs) {
     if (n_pairs < 1 || n_pairs > 32) return false;
     if (is_quant(kt) && qk_mode != kQkInt8) return false;  // f32-Q scores on quantized K stay on VALU
-    return mma_lookup(kt, d, (n_pairs + 15) / 16) != nullptr;
+    int w = 0;
+    return dec_lookup(kt, d, (n_pairs + 15) / 16, &w) != nullptr;
 }
 
-size_t fa_mma_qimg_bytes(int64_t n_rows, int kt, int d) { return (size_t)n_rows * mma_qrow_bytes(kt, d); }
+int fa_mma_waves(int kt, int d, int n_pairs) {
+    int w = 4;
+    if (!dec_lookup(kt, d, (n_pairs + 15) / 16, &w)) return 0;
+    return w;
+}
 
-hipError_t fa_mma_launch(const FaArgs& a, const FaLaunch& L, uint8_t* qimg, hipStream_t stream) {
-    const xq_tensor* q = L.q;
-    const int D = (int)q->ne[0];
+bool fa_mma_fused_merge(int64_t n_groups, int n_pairs, int n_splits) {
+    return n_splits > 1 && n_groups <= kMaxGroups && (int64_t)n_pairs * n_splits <= kFusedMergeMax;
+}
+
+hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
+    const int D = (int)L.q->ne[0];
     const int kt = L.k->type;
     const int mt = (a.QT * a.G + 15) / 16;
-    MmaPass1Fn p1 = mma_lookup(kt, D, mt);
-    MmaQprepFn qp = mma_qprep_lookup(kt, D);
-    if (!p1 || !qp) return hipErrorInvalidValue;
-    const int64_t n_rows = (int64_t)a.B * a.NQ * a.H;
-    const int hi_only = is_quant(kt) ? 0 : (L.q_round_f16 ? 1 : 0);
-    {
-        ProfScope ps("fa_qprep", stream);
-        hipLaunchKernelGGL(qp, dim3((uint32_t)n_rows), dim3(64), 0, stream, (const uint8_t*)q->data,
-                           (int64_t)q->nb[1], (int64_t)q->nb[2], (int64_t)q->nb[3], a.NQ, a.H, hi_only, qimg);
-    }
+    int waves = 0;
+    DecFn fn = dec_lookup(kt, D, mt, &waves);
+    if (!fn) return hipErrorInvalidValue;
+    a.q = (const uint8_t*)L.q->data;
+    a.q_nb1 = (int64_t)L.q->nb[1];
+    a.q_nb2 = (int64_t)L.q->nb[2];
+    a.q_nb3 = (int64_t)L.q->nb[3];
+    a.hi_only = is_quant(kt) ? 0 : (L.q_round_f16 ? 1 : 0);
+    const int64_t n_groups = (int64_t)a.B * a.Hkv * a.n_qtiles;
+    a.fused_merge = fa_mma_fused_merge(n_groups, a.QT * a.G, a.n_splits) ? 1 : 0;
+    // 4-row mask groups start at multiples of 4 rows; 8-byte reads need every
+    // row base 8-byte aligned
+    a.mask_vec = a.mask && ((uintptr_t)a.mask % 8) == 0 && a.m_nb1 % 8 == 0 && a.m_nb2 % 8 == 0 &&
+                 a.m_nb3 % 8 == 0 && a.split_rows % 4 == 0;
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
-    ProfScope ps("fa_pass1", stream);
-    hipLaunchKernelGGL(p1, dim3(n_wg), dim3(kThreads), 0, stream, a, (const uint8_t*)qimg, hi_only);
-    return hipGetLastError();
+    {
+        ProfScope ps("fa_dec", stream);
+        hipLaunchKernelGGL(fn, dim3(n_wg), dim3(64 * waves), 0, stream, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.n_splits == 1 || a.fused_merge) return e;
+    return fa_reduce_launch(a, D, stream);
 }
 
 }  // namespace xq

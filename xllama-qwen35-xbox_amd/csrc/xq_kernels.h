@@ -80,7 +80,6 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream);
 // Whether a compiled kernel exists for this combination.
 bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs);
 bool fa_mma_available(int kt, int d, int qk_mode, int n_pairs);
-size_t fa_mma_qimg_bytes(int64_t n_rows, int kt, int d);
 
 // ---------------------------------------------------------------- gdn
 
