@@ -11,10 +11,14 @@ One "step" is one call of the op on inputs already resident in HBM. Input sets
 are rotated (>= 512 MiB in total) so the 256 MB Infinity Cache cannot serve
 repeats. Reported:
   value        whole-call algorithmic HBM GB/s of the FA decode (bytes the op
-               must move once: K + V + Q + O + mask) / event-timed µs per call;
-  roofline     the dominant kernel (fa_pass1) alone: algorithmic bytes of one
-               launch / its average device duration from HIP events recorded
-               around each launch on the library's stream; peak 8 TB/s;
+               must move once: K + V + Q + O + mask) / µs per call, timed over
+               HIP-graph replays of calls on rotated input sets;
+  roofline     the dominant kernel (fa_dec, the whole call in one launch):
+               algorithmic bytes of one launch / its average device duration
+               from HIP events recorded around each launch on the stream it is
+               launched on; peak 8 TB/s; traffic = HBM bytes per launch from
+               the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+               (profiles/, scaled by the same counters on a plain copy), else null;
   cpu_baseline the ggml-CPU restatement (oracle/, "port") on the host cores of
                this box, on the same workload bytes.
 Synthetic data: torch's device generator for N(0,1) K/V rows, quantised on the
@@ -110,6 +114,92 @@ def time_calls(torch, fn, n_sets, steps, warmup):
     return start.elapsed_time(stop) / steps  # ms per call
 
 
+def graph_time(torch, fn, n_sets, steps, warmup):
+    """ms per call: the n_sets calls captured once in a HIP graph, replayed until
+    `steps` calls ran (after `warmup` eager calls)."""
+    for i in range(max(warmup, n_sets)):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(n_sets):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, math.ceil(steps / n_sets))
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / (reps * n_sets), reps * n_sets
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch from a committed counter summary (a JSON line in
+    profiles/<kernel>_<workload>_traffic.md), or None."""
+    path = ROOT / "profiles" / f"{kernel}_{workload}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        line = line.strip()
+        if line.startswith("{") and '"traffic_bytes"' in line:
+            return json.loads(line)
+    return None
+
+
+def summarize_pmc(fetch_dir, write_dir, kernel, workload, copy_bytes, command):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE of `kernel`, scaled by what the same
+    counters read for the plain device copy of `copy_bytes` in the same runs."""
+    import csv
+    import glob
+
+    def per_dispatch(d, counter):
+        vals = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                if r["Counter_Name"] != counter:
+                    continue
+                name = r["Kernel_Name"]
+                key = "copy" if ("copy" in name.lower() and "xq::" not in name) else name
+                vals.setdefault(key, {}).setdefault(r.get("Dispatch_Id", len(vals)), 0.0)
+                vals[key][r.get("Dispatch_Id", len(vals))] += float(r["Counter_Value"])
+        return vals
+
+    out = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        vals = per_dispatch(d, counter)
+        kern = [v for k, v in vals.items() if kernel in k]
+        copies = vals.get("copy", {})
+        if not kern or not copies:
+            raise SystemExit(f"{counter}: kernel {kernel!r} or the calibration copy not found in {d}")
+        kv = [x for v in kern for x in v.values()]
+        cv = list(copies.values())
+        k_kib = statistics.mean(kv)
+        c_kib = max(cv)  # the 512 MiB calibration copy is the largest copy dispatch
+        out[counter] = {"kernel_kib_per_dispatch": k_kib, "copy_kib": c_kib, "dispatches": len(kv)}
+    f_scale = copy_bytes / (out["FETCH_SIZE"]["copy_kib"] * 1024)
+    w_scale = copy_bytes / (out["WRITE_SIZE"]["copy_kib"] * 1024)
+    fetch = out["FETCH_SIZE"]["kernel_kib_per_dispatch"] * 1024 * f_scale
+    write = out["WRITE_SIZE"]["kernel_kib_per_dispatch"] * 1024 * w_scale
+    rec = {"kernel": kernel, "workload": workload, "traffic_bytes": round(fetch + write),
+           "fetch_bytes": round(fetch), "write_bytes": round(write),
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "raw": out}
+    lines = [f"# HBM traffic of {kernel} on {workload}", "",
+             "Commands (one counter per run; the 512 MiB torch copy in the same run calibrates the counter):", ""]
+    lines += [f"    {c}" for c in command]
+    lines += ["", f"FETCH_SIZE per dispatch {out['FETCH_SIZE']['kernel_kib_per_dispatch']:.0f} KiB over "
+                  f"{out['FETCH_SIZE']['dispatches']} dispatches; copy of {copy_bytes >> 20} MiB read "
+                  f"{out['FETCH_SIZE']['copy_kib']:.0f} KiB -> scale {f_scale:.4f}",
+              f"WRITE_SIZE per dispatch {out['WRITE_SIZE']['kernel_kib_per_dispatch']:.0f} KiB; copy wrote "
+              f"{out['WRITE_SIZE']['copy_kib']:.0f} KiB -> scale {w_scale:.4f}",
+              f"traffic per launch = {rec['traffic_bytes'] / 1e6:.2f} MB", "", json.dumps(rec)]
+    return rec, "\n".join(lines) + "\n"
+
+
 def kernel_times(torch, xq, fn, n_sets, steps):
     xq.profile_reset()
     xq.profile_enable(True)
@@ -174,7 +264,20 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work per baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
+    ap.add_argument("--only", choices=["fa", "gdn", "all"], default="all")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the traffic summary of fa_dec from two rocprofv3 --pmc output dirs and exit")
+    ap.add_argument("--pmc-command", action="append", default=[], help="command lines recorded in the summary")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        from xqattn import workloads as wl
+        rec, text = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], "fa_dec", wl.FA_C2.name,
+                                  512 << 20, args.pmc_command)
+        out = ROOT / "profiles" / f"fa_dec_{wl.FA_C2.name}_traffic.md"
+        out.parent.mkdir(exist_ok=True)
+        out.write_text(text)
+        print(json.dumps(rec))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -199,104 +302,106 @@ def main():
         log("calibration copy of 512 MiB done")
         del a, b
 
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+
     # ---------------- FA decode @32k q8_0 (headline)
     cfg = wl.FA_C2
-    n_sets = max(2, math.ceil(512 * 2**20 / cfg.kv_bytes()))
-    log(f"building {n_sets} input sets of {cfg.name} ({cfg.kv_bytes() / 1e6:.1f} MB KV each)")
-    sets = make_fa_sets(torch, xq, wl, cfg, n_sets)
-    params = xq.fa_params(cfg.kq_scale)
-    q, k, v, m, d = sets[0]
-    ws = torch.empty(xq.flash_attn_ext_workspace(q, k, v, m, None, d, params) + 256,
-                     dtype=torch.uint8, device="cuda")
-
-    def fa_call(i):
-        q, k, v, m, d = sets[i]
-        xq.flash_attn_ext(q, k, v, m, None, d, params, workspace=ws)
-
-    log(f"FA: warmup {args.warmup}, timing {args.steps} calls")
-    ms_call = time_calls(torch, fa_call, n_sets, args.steps, args.warmup)
-    kt = kernel_times(torch, xq, fa_call, n_sets, args.steps)
     alg = cfg.algorithmic_bytes()
-    gbs = alg / (ms_call * 1e-3) / 1e9
-    p1_us = kt.get("fa_pass1", {}).get("avg_us", float("nan"))
-    # pass 1 moves all the algorithmic bytes except the output row (written by the reduce)
-    p1_bytes = alg - cfg.B * cfg.n_q * cfg.H * cfg.D * 4
-    p1_gbs = p1_bytes / (p1_us * 1e-6) / 1e9
-    log(f"FA: {ms_call * 1000:.2f} us/call, {gbs:.0f} GB/s; kernels {kt}")
+    if args.only in ("fa", "all"):
+        n_sets = max(2, math.ceil(512 * 2**20 / cfg.kv_bytes()))
+        log(f"building {n_sets} input sets of {cfg.name} ({cfg.kv_bytes() / 1e6:.1f} MB KV each)")
+        sets = make_fa_sets(torch, xq, wl, cfg, n_sets)
+        params = xq.fa_params(cfg.kq_scale)
+        q, k, v, m, d = sets[0]
+        ws = torch.empty(xq.flash_attn_ext_workspace(q, k, v, m, None, d, params) + 256,
+                         dtype=torch.uint8, device="cuda")
+
+        def fa_call(i):
+            q, k, v, m, d = sets[i]
+            xq.flash_attn_ext(q, k, v, m, None, d, params, workspace=ws)
+
+        log(f"FA: warmup {args.warmup}, timing {args.steps} calls (graph replays)")
+        ms_call, n_timed = graph_time(torch, fa_call, n_sets, args.steps, args.warmup)
+        kt = kernel_times(torch, xq, fa_call, n_sets, args.steps)
+        gbs = alg / (ms_call * 1e-3) / 1e9
+        k_us = kt.get("fa_dec", {}).get("avg_us", float("nan"))
+        k_gbs = alg / (k_us * 1e-6) / 1e9
+        log(f"FA: {ms_call * 1000:.2f} us/call, {gbs:.0f} GB/s; kernels {kt}")
+        tr = traffic_from_profiles("fa_dec", cfg.name)
+        out.update({
+            "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms_call, 5),
+            "config": {"workload": cfg.name, "op": "GGML_OP_FLASH_ATTN_EXT", "kv_type": "q8_0", "n_q": cfg.n_q,
+                       "n_head": cfg.H, "n_head_kv": cfg.Hkv, "head_dim": cfg.D, "kv_len": cfg.L,
+                       "n_seq": cfg.B, "mask": "f16 all-visible", "input_sets": n_sets, "timed_calls": n_timed,
+                       "compute": "int8 MFMA q8_0 scores, f16 MFMA values, f32 online softmax and accumulation"},
+            "us_per_call": round(ms_call * 1000, 2),
+            "pct_of_8TBs": round(100 * gbs / PEAK_GBS, 1),
+            "tokens_per_s_equiv": round(cfg.B * cfg.n_q / (ms_call * 1e-3), 1),
+            "algorithmic_bytes": alg,
+            "roofline": {"bound": "hbm", "kernel": "fa_dec", "achieved": round(k_gbs, 1), "peak": PEAK_GBS,
+                         "unit": "GB/s", "frac": round(k_gbs / PEAK_GBS, 4),
+                         "traffic": tr["traffic_bytes"] if tr else None,
+                         "bytes_per_launch": alg, "avg_launch_us": round(k_us, 3)},
+            "kernels": kt,
+        })
 
     # ---------------- GDN decode step
     gcfg = wl.GDN_C3
-    g_sets_n = max(2, math.ceil(512 * 2**20 / gcfg.algorithmic_bytes()))
-    log(f"building {g_sets_n} GDN input sets")
-    gsets = make_gdn_sets(torch, xq, wl, gcfg, g_sets_n)
+    if args.only in ("gdn", "all"):
+        g_sets_n = max(2, math.ceil(512 * 2**20 / gcfg.algorithmic_bytes()))
+        log(f"building {g_sets_n} GDN input sets")
+        gsets = make_gdn_sets(torch, xq, wl, gcfg, g_sets_n)
 
-    def gdn_call(i):
-        xq.gated_delta_net(*gsets[i], gcfg.slots, mode=xq.GDN_STEP)
+        def gdn_call(i):
+            xq.gated_delta_net(*gsets[i], gcfg.slots, mode=xq.GDN_STEP)
 
-    g_ms = time_calls(torch, gdn_call, g_sets_n, max(args.steps, 100), args.warmup)
-    gkt = kernel_times(torch, xq, gdn_call, g_sets_n, max(args.steps, 100))
-    g_alg = gcfg.algorithmic_bytes()
-    g_kus = gkt.get("gdn_step", {}).get("avg_us", float("nan"))
-    log(f"GDN: {g_ms * 1000:.2f} us/call, kernel {g_kus:.2f} us")
+        g_ms, _ = graph_time(torch, gdn_call, g_sets_n, max(args.steps, 100), args.warmup)
+        gkt = kernel_times(torch, xq, gdn_call, g_sets_n, max(args.steps, 100))
+        g_alg = gcfg.algorithmic_bytes()
+        g_kus = gkt.get("gdn_step", {}).get("avg_us", float("nan"))
+        log(f"GDN: {g_ms * 1000:.2f} us/call, kernel {g_kus:.2f} us")
+        out["gdn_step"] = {"workload": gcfg.name, "us_per_call": round(g_ms * 1000, 3),
+                           "kernel_avg_us": round(g_kus, 3), "algorithmic_bytes": g_alg,
+                           "GB/s": round(g_alg / (g_kus * 1e-6) / 1e9, 1),
+                           "frac": round(g_alg / (g_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
+                           "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "input_sets": g_sets_n}
+        if args.only == "gdn":
+            out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                        "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})
 
     # ---------------- CPU baselines (ggml-CPU semantics restated, this host's cores)
-    cpu = None
-    gdn_cpu = None
     if not args.no_cpu:
         try:
             threads = len(os.sched_getaffinity(0))
         except AttributeError:
             threads = os.cpu_count() or 1
         threads = max(1, min(threads, 16))
-        fa_call(0)
-        torch.cuda.synchronize()
-        log(f"CPU baseline: FA on {threads} threads")
-        t_cpu, n_cpu, max_err = cpu_fa_baseline(torch, wl, cfg, sets[0], threads, args.cpu_budget)
-        cpu = {"value": round(alg / t_cpu / 1e9, 3), "unit": "GB/s", "us_per_call": round(t_cpu * 1e6, 1),
-               "cores": threads, "kind": "port",
-               "sample": f"the full {cfg.name} call (same q8_0 bytes), oracle/xq_oracle.c ggml one-chunk loop, "
-                         f"median of {n_cpu} runs",
-               "gpu_vs_cpu_max_abs_err": max_err}
-        gdn_call(0)
-        torch.cuda.synchronize()
-        log(f"CPU baseline: GDN on {threads} threads")
-        t_g, n_g, g_err = cpu_gdn_baseline(torch, wl, gsets[0], gcfg.slots, threads, args.cpu_budget / 2)
-        gdn_cpu = {"us_per_call": round(t_g * 1e6, 1), "cores": threads, "kind": "port",
-                   "GB/s": round(g_alg / t_g / 1e9, 3), "median_of": n_g, "gpu_vs_cpu_max_abs_err": g_err}
-
-    out = {
-        "metric": METRIC,
-        "value": round(gbs, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_call, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {"workload": cfg.name, "op": "GGML_OP_FLASH_ATTN_EXT", "kv_type": "q8_0", "n_q": cfg.n_q,
-                   "n_head": cfg.H, "n_head_kv": cfg.Hkv, "head_dim": cfg.D, "kv_len": cfg.L,
-                   "n_seq": cfg.B, "mask": "f16 all-visible", "input_sets": n_sets,
-                   "compute": "int8 dot4 q8_0 scores, f32 online softmax and value accumulation"},
-        "us_per_call": round(ms_call * 1000, 2),
-        "pct_of_8TBs": round(100 * gbs / PEAK_GBS, 1),
-        "tokens_per_s_equiv": round(cfg.B * cfg.n_q / (ms_call * 1e-3), 1),
-        "algorithmic_bytes": alg,
-        "roofline": {"bound": "hbm", "kernel": "fa_pass1", "achieved": round(p1_gbs, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(p1_gbs / PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": p1_bytes, "avg_launch_us": round(p1_us, 3)},
-        "kernels": kt,
-        "cpu_baseline": cpu,
-        "gdn_step": {"workload": gcfg.name, "us_per_call": round(g_ms * 1000, 3),
-                     "kernel_avg_us": round(g_kus, 3), "algorithmic_bytes": g_alg,
-                     "GB/s": round(g_alg / (g_kus * 1e-6) / 1e9, 1),
-                     "frac": round(g_alg / (g_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
-                     "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1),
-                     "input_sets": g_sets_n, "cpu_baseline": gdn_cpu},
-    }
+        if args.only in ("fa", "all"):
+            fa_call(0)
+            torch.cuda.synchronize()
+            log(f"CPU baseline: FA on {threads} threads")
+            t_cpu, n_cpu, max_err = cpu_fa_baseline(torch, wl, cfg, sets[0], threads, args.cpu_budget)
+            out["cpu_baseline"] = {
+                "value": round(alg / t_cpu / 1e9, 3), "unit": "GB/s", "us_per_call": round(t_cpu * 1e6, 1),
+                "cores": threads, "kind": "port",
+                "sample": f"the full {cfg.name} call (same q8_0 bytes), oracle/xq_oracle.c ggml one-chunk "
+                          f"loop, median of {n_cpu} runs",
+                "gpu_vs_cpu_max_abs_err": max_err}
+        if args.only in ("gdn", "all"):
+            gdn_call(0)
+            torch.cuda.synchronize()
+            log(f"CPU baseline: GDN on {threads} threads")
+            t_g, n_g, g_err = cpu_gdn_baseline(torch, wl, gsets[0], gcfg.slots, threads, args.cpu_budget / 2)
+            gdn_cpu = {"us_per_call": round(t_g * 1e6, 1), "cores": threads, "kind": "port",
+                       "GB/s": round(gcfg.algorithmic_bytes() / t_g / 1e9, 3), "median_of": n_g,
+                       "gpu_vs_cpu_max_abs_err": g_err}
+            out["gdn_step"]["cpu_baseline"] = gdn_cpu
+            if args.only == "gdn":
+                out["cpu_baseline"] = {"value": gdn_cpu["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+                                       "sample": f"the full {gcfg.name} step, median of {n_g} runs"}
+    else:
+        out.setdefault("cpu_baseline", None)
     print(json.dumps(out), flush=True)
 
 

@@ -183,3 +183,18 @@ def test_fa_range_vs_reference_semantics(torch_gpu, kv_type, active):
     assert_close(got, want, atol=3e-4, rtol=3e-4, what="range O")
     assert_close(glse, wlse, atol=3e-4, rtol=3e-5, what="range LSE")
     assert np.all(got[1] == 0.0) and np.all(np.isneginf(glse[1])), "query before origin must be empty"
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+def test_fa_empty_trailing_split(torch_gpu, engine):
+    """The reference's fine mode keeps 256 splits at 10200 rows (40 rows each), so
+    the last split is empty; its partial state must merge as nothing."""
+    assert xqattn.split_count(10200, xqattn.SPLIT_FINE) == 256
+    assert xqattn.split_rows(10200, xqattn.SPLIT_FINE) * 255 >= 10200
+    cfg = wl.FaConfig("q8_empty_split", 1, 8, 2, 128, 10200, 1, wl.Q8_0)
+    case_note(f"empty trailing split engine {engine}")
+    case = make_fa_case(cfg, seed=13)
+    got, glse = run_gpu(case, torch_gpu, split_mode=xqattn.SPLIT_FINE, engine=engine)
+    ref64, lse64 = oracle_f64(case)
+    assert_close(got, ref64, atol=5e-4, rtol=5e-4, what="empty trailing split")
+    assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what="empty trailing split LSE")

@@ -88,34 +88,36 @@ void split_policy(int64_t L, int mode, int64_t n_seq_heads, int32_t* n_splits, i
         *rows = 1;
         return;
     }
-    int64_t r = L;
+    int64_t r = L, k = 1;
     switch (mode) {
     case XQ_FA_SPLIT_AUTO: {
         // about one workgroup per CU (256 on MI355X) over the (sequence, KV
         // head) pairs, rows a multiple of the 16-row wave slice
-        int64_t k = cdiv(256, n_seq_heads < 1 ? 1 : n_seq_heads);
+        k = cdiv(256, n_seq_heads < 1 ? 1 : n_seq_heads);
         const int64_t kmax = cdiv(L, 16);
         if (k > kmax) k = kmax;
         if (k > 256) k = 256;
         if (k < 1) k = 1;
         r = cdiv(cdiv(L, k), 16) * 16;
+        k = cdiv(L, r);
         break;
     }
-    case XQ_FA_SPLIT_REFERENCE: {
-        int64_t k = cdiv(L, 256);
+    // the reference's modes keep their k even when the last split is empty
+    // (rows * (k - 1) >= L happens, e.g. 58128 rows in the fine mode)
+    case XQ_FA_SPLIT_REFERENCE:
+        k = cdiv(L, 256);
         if (k > 32) k = 32;
         if (k < 1) k = 1;
         r = cdiv(L, k);
         break;
-    }
-    case XQ_FA_SPLIT_BALANCED: r = cdiv(L, opt_split_k(L, 1)); break;
-    case XQ_FA_SPLIT_FINE: r = cdiv(L, opt_split_k(L, 2)); break;
-    case XQ_FA_SPLIT_COARSE: r = cdiv(L, opt_split_k(L, 3)); break;
+    case XQ_FA_SPLIT_BALANCED: k = opt_split_k(L, 1); r = cdiv(L, k); break;
+    case XQ_FA_SPLIT_FINE: k = opt_split_k(L, 2); r = cdiv(L, k); break;
+    case XQ_FA_SPLIT_COARSE: k = opt_split_k(L, 3); r = cdiv(L, k); break;
     case XQ_FA_SPLIT_NONE:
-    default: r = L; break;
+    default: r = L; k = 1; break;
     }
     *rows = r;
-    *n_splits = (int32_t)cdiv(L, r);
+    *n_splits = (int32_t)k;
 }
 
 // ------------------------------------------------------------ FA contract
