@@ -20,8 +20,12 @@
  * point allocates device memory: scratch comes from a caller-owned workspace
  * whose size is returned by the *_workspace queries. Errors are returned as
  * xq_status codes (never abort); xq_last_error() gives a message for the
- * calling thread. Calls on different streams are reentrant; calls sharing one
- * workspace buffer must be ordered by the caller.
+ * calling thread. Calls sharing one workspace buffer must be ordered by the
+ * caller. xq_flash_attn_ext calls with more than one KV split merge their
+ * splits inside the kernel through an arrival-counter array the library keeps
+ * per device (zero at load, left at zero by every completed call): two such
+ * calls must not run concurrently on one device (calls on one stream, or
+ * inside one captured graph, are ordered and safe).
  */
 #ifndef XQ_ATTN_H
 #define XQ_ATTN_H

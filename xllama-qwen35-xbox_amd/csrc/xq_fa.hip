@@ -21,8 +21,8 @@
 //               then applies sinks and the 1/S normalisation.
 //
 // Every (query, head) pair runs the same instruction sequence whatever other
-// pairs share its workgroup, and the split partition depends on the KV length
-// only, so a query's result is bitwise independent of the query count of the
+// pairs share its workgroup, and the split partition never depends on the
+// number of queries, so a query's result is bitwise independent of the query count of the
 // call (the purpose of patches/0006-…:7-11 and patches/0008-…:40-56). The
 // kernels are compiled with -ffp-contract=off and write every fused
 // multiply-add explicitly.
