@@ -198,3 +198,34 @@ def test_fa_empty_trailing_split(torch_gpu, engine):
     ref64, lse64 = oracle_f64(case)
     assert_close(got, ref64, atol=5e-4, rtol=5e-4, what="empty trailing split")
     assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what="empty trailing split LSE")
+
+
+def test_fa_graph_replays_match_eager(torch_gpu):
+    """A captured multi-split call replays bit-identically (the in-kernel split
+    merge leaves its arrival counters at zero after every call)."""
+    torch = torch_gpu
+    cfg = wl.FaConfig("q8_graph", 1, 24, 4, 256, 6000, 2, wl.Q8_0)
+    case_note("graph replays")
+    case = make_fa_case(cfg, seed=17)
+    q, k, v = (xqattn.DevTensor.from_host(t) for t in (case.q, case.k, case.v))
+    m = xqattn.DevTensor.from_host(case.mask)
+    d = xqattn.DevTensor.empty_like_host(case.dst)
+    p = xqattn.fa_params(case.scale)
+    ws = torch.zeros(xqattn.flash_attn_ext_workspace(q, k, v, m, None, d, p) + 256, dtype=torch.uint8,
+                     device="cuda")
+    xqattn.flash_attn_ext(q, k, v, m, None, d, p, workspace=ws)
+    torch.cuda.synchronize()
+    eager = d.to_host_bytes().copy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        xqattn.flash_attn_ext(q, k, v, m, None, d, p, workspace=ws)
+    for rep in range(4):
+        d.t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(d.to_host_bytes(), eager), f"replay {rep} differs"
+        xqattn.flash_attn_ext(q, k, v, m, None, d, p, workspace=ws)  # eager work between replays
+        torch.cuda.synchronize()
