@@ -161,6 +161,27 @@ def test_gdn_predicate():
     assert l.xq_supports_gated_delta_net(args[0], args[1], ctypes.byref(v_bad), *args[3:], 1, 0) == 0
 
 
+def test_gdn_workspace_query():
+    """AUTO runs prefills longer than one chunk on the chunked kernels: one
+    workspace record of 115712 bytes per (sequence, v-head, 64-token chunk) of
+    the first T - (slots - 1) tokens; the step kernel needs none."""
+    l = lib()
+    n = ctypes.c_size_t(0)
+
+    def need(T, B, slots, mode):
+        q = _desc(wl.BF16, (128, 16, T, B))
+        v = _desc(wl.BF16, (128, 32, T, B))
+        assert l.xq_gated_delta_net_workspace(ctypes.byref(q), ctypes.byref(v), slots, mode, ctypes.byref(n)) == 0
+        return n.value
+
+    rec = 115712
+    assert need(200, 2, 3, xqattn.GDN_CHUNKED) == 2 * 32 * 4 * rec  # 198 tokens -> 4 chunks
+    assert need(4096, 1, 1, xqattn.GDN_AUTO) == 32 * 64 * rec
+    assert need(64, 1, 1, xqattn.GDN_AUTO) == 0                     # one chunk: step kernel
+    assert need(4096, 1, 1, xqattn.GDN_STEP) == 0
+    assert need(3, 1, 5, xqattn.GDN_CHUNKED) == 0                   # every token keeps a snapshot
+
+
 @pytest.mark.parametrize("typ,d,want", [(wl.F16, 128, 256), (wl.Q8_0, 256, 272), (wl.Q8_0, 128, 136),
                                         (wl.Q4_0, 128, 72), (wl.E5M2, 256, 256), (wl.F32, 128, 512)])
 def test_kv_record_bytes(typ, d, want):

@@ -1,0 +1,93 @@
+"""GPU parity of the chunked GATED_DELTA_NET prefill (64-token WY/UT chunks on
+the matrix cores) against the token-sequential recurrence: the CPU restatement
+of the reference's op (src/bridge/ggml_d3d12.cpp:113-158) and a float64
+recurrence.
+
+Covers the full prefill (4096 bf16 tokens), partial last chunks, snapshot slots
+(the last slots - 1 tokens run on the step kernel from the chunked part's
+state), f32 and bf16 inputs, padded q/k/v rows and several sequences.
+
+Tolerance (north star): outputs and states within max-abs 2e-3 / rel 1e-2.
+"""
+import numpy as np
+import pytest
+
+import xqattn
+from conftest import assert_close, case_note
+from gdn_cases import SENTINEL, make_gdn_case
+from test_gpu_gdn import run_gpu
+from xqattn import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+
+def _valid_rows(case):
+    return case.T + 128 * min(case.T, case.slots)
+
+
+def _check(case, got, want, what):
+    v = _valid_rows(case)
+    err = assert_close(got[:, :v], want[:, :v], what=what)
+    assert np.all(got[:, v:] == SENTINEL), f"{what}: an unwritten snapshot slot was overwritten"
+    return err
+
+
+def test_gdn_chunked_prefill_4096_bf16(torch_gpu):
+    cfg = wl.GDN_C4
+    case_note(f"gated_delta_net chunked {cfg.name}")
+    case = make_gdn_case(cfg.T, cfg.slots, B=cfg.B, dist="north_star", bf16=cfg.bf16, seed=77)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    err = _check(case, got, case.oracle(), "C4 chunked vs restated recurrence")
+    err64 = _check(case, got, case.oracle_f64(), "C4 chunked vs float64")
+    print(f"C4: max|gpu-oracle|={err:.2e} max|gpu-f64|={err64:.2e}")
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("T,slots,B", [(65, 1, 1), (100, 1, 2), (128, 1, 1), (130, 3, 1),
+                                       (200, 17, 1), (257, 5, 2), (64, 1, 1), (7, 2, 1)])
+def test_gdn_chunked_shapes(torch_gpu, T, slots, B, bf16):
+    case_note(f"gdn chunked T={T} slots={slots} B={B} bf16={bf16}")
+    case = make_gdn_case(T, slots, B=B, dist="north_star", bf16=bf16, seed=T + 31 * slots)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    err = _check(case, got, case.oracle_f64(), f"chunked T={T} K={slots} B={B}")
+    print(f"T={T} K={slots} B={B} bf16={bf16}: max|gpu-f64|={err:.2e}")
+
+
+@pytest.mark.parametrize("T,slots", [(5, 5), (5, 1), (3, 5), (64, 5), (70, 5), (70, 1)])
+def test_gdn_chunked_selftest_inputs(torch_gpu, T, slots):
+    """The reference selftest's input recipe through the chunked mode (with
+    T < slots every token keeps a snapshot and the step kernel runs alone)."""
+    case_note(f"gdn chunked selftest T={T} K={slots}")
+    case = make_gdn_case(T, slots, B=1, dist="selftest")
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    _check(case, got, case.oracle(), f"chunked selftest T={T} K={slots}")
+
+
+@pytest.mark.parametrize("pad", [3, 8])
+def test_gdn_chunked_padded_rows(torch_gpu, pad):
+    case = make_gdn_case(150, 2, B=2, dist="north_star", pad=pad, seed=3)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    _check(case, got, case.oracle_f64(), f"chunked padded rows pad={pad}")
+
+
+def test_gdn_chunked_matches_step_kernel(torch_gpu):
+    """Both kernels compute the same recurrence; AUTO picks the chunked one
+    for prefills longer than one chunk."""
+    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=True, seed=12)
+    a = run_gpu(case, torch_gpu, mode=xqattn.GDN_STEP)
+    b = run_gpu(case, torch_gpu, mode=xqattn.GDN_AUTO)
+    c = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    assert np.array_equal(b, c)
+    _check(case, c, a, "chunked vs step kernel")
+
+
+def test_gdn_chunked_strong_decay(torch_gpu):
+    """Decays that underflow within a chunk (g = -40 per token) keep every
+    factor in [0, 1] and the result finite."""
+    case = make_gdn_case(192, 1, B=1, dist="north_star", seed=21)
+    g = np.frombuffer(case.g.buf.tobytes(), np.float32).copy()
+    g[::3] = -40.0
+    case.g.buf[:] = g.view(np.uint8)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    _check(case, got, case.oracle_f64(), "chunked strong decay")
+

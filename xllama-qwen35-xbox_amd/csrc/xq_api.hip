@@ -425,11 +425,10 @@ static int gdn_pick(int32_t mode, int64_t T) {
 
 xq_status xq_gated_delta_net_workspace(const xq_tensor* q, const xq_tensor* v, int32_t slots,
                                        int32_t mode, size_t* bytes) {
-    (void)slots;
     if (!q || !v || !bytes) return fail(XQ_ERR_BAD_ARG, "null argument");
     if (mode < XQ_GDN_AUTO || mode > XQ_GDN_CHUNKED) return fail(XQ_ERR_BAD_ARG, "bad mode");
     const int64_t T = v->ne[2], B = v->ne[3];
-    *bytes = gdn_pick(mode, T) == XQ_GDN_CHUNKED ? xq::gdn_chunked_workspace_bytes(T, B) : 0;
+    *bytes = gdn_pick(mode, T) == XQ_GDN_CHUNKED ? xq::gdn_chunked_workspace_bytes(T, B, slots) : 0;
     return ok();
 }
 
@@ -450,7 +449,7 @@ xq_status xq_gated_delta_net(const xq_tensor* q, const xq_tensor* k, const xq_te
     const int64_t T = v->ne[2], B = v->ne[3];
     hipError_t e;
     if (gdn_pick(mode, T) == XQ_GDN_CHUNKED) {
-        const size_t need = xq::gdn_chunked_workspace_bytes(T, B);
+        const size_t need = xq::gdn_chunked_workspace_bytes(T, B, slots);
         if (need && (!workspace || workspace_bytes < need))
             return fail(XQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
         e = xq::gdn_chunked_launch(L, (hipStream_t)stream);

@@ -198,12 +198,3 @@ hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
 
 }  // namespace xq
 
-namespace xq {
-
-// The chunked (WY/UT, bf16 MFMA) prefill lives in xq_gdn_chunked.hip once
-// built; until then CHUNKED mode is reported as unsupported.
-size_t gdn_chunked_workspace_bytes(int64_t, int64_t) { return 0; }
-hipError_t gdn_chunked_launch(const GdnLaunch&, hipStream_t) { return hipErrorNotSupported; }
-bool gdn_chunked_available() { return false; }
-
-}  // namespace xq
