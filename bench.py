@@ -79,6 +79,8 @@ def make_fa_sets(torch, xq, wl, cfg, n_sets, seed=0):
 
 
 def make_gdn_sets(torch, xq, wl, cfg, n_sets, seed=1):
+    """q, k L2-normalised N(0,1), v ~ N(0,1), beta = sigmoid(N(0,1)),
+    g = -softplus(N(0,1)), state ~ 0.1 N(0,1); q/k/v in bf16 when cfg.bf16."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     B, T, K = cfg.B, cfg.T, cfg.slots
@@ -93,8 +95,13 @@ def make_gdn_sets(torch, xq, wl, cfg, n_sets, seed=1):
         rows = T + K * 128
         dst = torch.empty((B, rows, 4096), dtype=torch.float32, device="cuda")
         F = wl.F32
-        mk = lambda t, ne: xq.DevTensor(F, ne, (4, 4 * ne[0], 4 * ne[0] * ne[1], 4 * ne[0] * ne[1] * ne[2]), t)
-        sets.append((mk(qf, (128, 16, T, B)), mk(kf, (128, 16, T, B)), mk(vf, (128, 32, T, B)),
+        mk = lambda t, ne, typ=F, es=4: xq.DevTensor(typ, ne, (es, es * ne[0], es * ne[0] * ne[1],
+                                                               es * ne[0] * ne[1] * ne[2]), t)
+        if cfg.bf16:
+            qkv = lambda t, ne: mk(t.to(torch.bfloat16).contiguous(), ne, wl.BF16, 2)
+        else:
+            qkv = mk
+        sets.append((qkv(qf, (128, 16, T, B)), qkv(kf, (128, 16, T, B)), qkv(vf, (128, 32, T, B)),
                      mk(g, (1, 32, T, B)), mk(beta, (1, 32, T, B)), mk(st, (128, 128, 32, B)),
                      xq.DevTensor(F, (4096, rows, B, 1), (4, 16384, 16384 * rows, 16384 * rows * B), dst)))
     torch.cuda.synchronize()
@@ -264,7 +271,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work per baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
-    ap.add_argument("--only", choices=["fa", "gdn", "all"], default="all")
+    ap.add_argument("--only", choices=["fa", "gdn", "prefill", "all"], default="all")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary of fa_dec from two rocprofv3 --pmc output dirs and exit")
     ap.add_argument("--pmc-command", action="append", default=[], help="command lines recorded in the summary")
@@ -370,6 +377,33 @@ def main():
             out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})
 
+    # ---------------- GDN chunked prefill (4096 bf16 tokens, one sequence)
+    pcfg = wl.GDN_C4
+    if args.only in ("prefill", "all"):
+        p_sets_n = 2
+        log(f"building {p_sets_n} GDN prefill input sets ({pcfg.name})")
+        psets = make_gdn_sets(torch, xq, wl, pcfg, p_sets_n, seed=3)
+        q0, _, v0 = psets[0][:3]
+        p_ws = torch.empty(xq.gated_delta_net_workspace(q0, v0, pcfg.slots, xq.GDN_CHUNKED) + 256,
+                           dtype=torch.uint8, device="cuda")
+
+        def prefill_call(i):
+            xq.gated_delta_net(*psets[i], pcfg.slots, mode=xq.GDN_CHUNKED, workspace=p_ws)
+
+        p_steps = max(args.steps // 2, 10)
+        p_ms, _ = graph_time(torch, prefill_call, p_sets_n, p_steps, args.warmup)
+        pkt = kernel_times(torch, xq, prefill_call, p_sets_n, p_steps)
+        p_alg = pcfg.algorithmic_bytes()
+        log(f"GDN prefill: {p_ms * 1000:.2f} us/call; kernels {pkt}")
+        out["gdn_prefill"] = {"workload": pcfg.name, "us_per_call": round(p_ms * 1000, 3),
+                              "algorithmic_bytes": p_alg, "call_GB/s": round(p_alg / (p_ms * 1e-3) / 1e9, 1),
+                              "frac_of_hbm_roofline": round(p_alg / (p_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                              "tokens_per_s": round(pcfg.T * pcfg.B / (p_ms * 1e-3), 1),
+                              "kernels": pkt, "workspace_bytes": int(p_ws.numel())}
+        if args.only == "prefill":
+            out.update({"value": round(p_alg / (p_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+                        "ms_per_step": round(p_ms, 5), "config": {"workload": pcfg.name}})
+
     # ---------------- CPU baselines (ggml-CPU semantics restated, this host's cores)
     if not args.no_cpu:
         try:
@@ -400,6 +434,19 @@ def main():
             if args.only == "gdn":
                 out["cpu_baseline"] = {"value": gdn_cpu["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
                                        "sample": f"the full {gcfg.name} step, median of {n_g} runs"}
+        if args.only in ("prefill", "all"):
+            prefill_call(0)
+            torch.cuda.synchronize()
+            log(f"CPU baseline: GDN prefill on {threads} threads")
+            t_p, n_p, p_err = cpu_gdn_baseline(torch, wl, psets[0], pcfg.slots, threads, args.cpu_budget / 4)
+            p_cpu = {"us_per_call": round(t_p * 1e6, 1), "cores": threads, "kind": "port",
+                     "GB/s": round(pcfg.algorithmic_bytes() / t_p / 1e9, 3), "median_of": n_p,
+                     "gpu_vs_cpu_max_abs_err": p_err}
+            out["gdn_prefill"]["cpu_baseline"] = p_cpu
+            if args.only == "prefill":
+                out["cpu_baseline"] = {"value": p_cpu["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
+                                       "sample": f"the full {pcfg.name} prefill (sequential recurrence), "
+                                                 f"median of {n_p} runs"}
     else:
         out.setdefault("cpu_baseline", None)
     print(json.dumps(out), flush=True)

@@ -260,6 +260,15 @@ def supports_gated_delta_net(q, k, v, g, beta, state, dst, slots, raw_gates=0) -
     return bool(load().xq_supports_gated_delta_net(*[ctypes.byref(x) for x in ds], slots, raw_gates))
 
 
+def gated_delta_net_workspace(q, v, slots, mode=GDN_AUTO) -> int:
+    """Device workspace bytes xq_gated_delta_net needs for these shapes and mode."""
+    n = ctypes.c_size_t(0)
+    dq, dv = q.desc(), v.desc()
+    _check(load().xq_gated_delta_net_workspace(ctypes.byref(dq), ctypes.byref(dv), slots, mode,
+                                               ctypes.byref(n)), "gated_delta_net_workspace")
+    return int(n.value)
+
+
 def gated_delta_net(q, k, v, g, beta, state, dst, slots, mode=GDN_AUTO, raw_gates=0,
                     workspace=None, stream=None):
     lib = load()
