@@ -11,8 +11,6 @@
 // and each kept snapshot written once.
 #include "xq_kernels.h"
 
-#include <stdlib.h>
-
 namespace xq {
 
 struct GdnStepArgs {
@@ -69,9 +67,71 @@ XQ_DEV void ld_row8(const uint8_t* p, int li, float (&x)[8]) {
     }
 }
 
-// CPT state columns per 16-lane row (column c_j = base + row + 16*j); their
-// state loads are all issued before any compute so they are in flight together.
+// Inputs of one token as one row of a workgroup needs them.
+template <int CPT>
+struct StepIn {
+    float q[8], k[8], v[CPT], g, beta;
+};
+
 template <bool BF16, bool VEC, int CPT>
+XQ_DEV void load_token(const GdnStepArgs& a, int b, int h, int kh, int li, int col0, int t, StepIn<CPT>& in) {
+    ld_row8<BF16, VEC>(a.q + (int64_t)b * a.q_nb3 + (int64_t)t * a.q_nb2 + (int64_t)kh * a.q_nb1, li, in.q);
+    ld_row8<BF16, VEC>(a.k + (int64_t)b * a.k_nb3 + (int64_t)t * a.k_nb2 + (int64_t)kh * a.k_nb1, li, in.k);
+    const uint8_t* vrow = a.v + (int64_t)b * a.v_nb3 + (int64_t)t * a.v_nb2 + (int64_t)h * a.v_nb1;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) in.v[j] = ld_elem<BF16>(vrow, col0 + 16 * j);
+    in.g = *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)t * a.g_nb2 + (int64_t)h * a.g_nb1);
+    in.beta = *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)t * a.b_nb2 + (int64_t)h * a.b_nb1);
+}
+
+// One token through CPT state columns of a row (column c_j = col0 + 16*j):
+// decay, delta rule, output, and the snapshot when the token keeps one. A
+// single token (ONE) always keeps its state, in slot 0.
+template <int CPT, bool ONE>
+XQ_DEV void step_token(const GdnStepArgs& a, const StepIn<CPT>& in, float4 (&s0)[CPT], float4 (&s1)[CPT],
+                       float* out, int h, int li, int col0, int t) {
+    const float decay = expf(in.g);
+    const int slot = a.T - 1 - t;
+    const bool keep = ONE || (a.slots > 1 && slot < a.slots) || (a.slots == 1 && t + 1 == a.T);
+    const int64_t s_off = (int64_t)4096 * a.T;
+    const int64_t slot_off = ONE || a.slots == 1 ? 0 : (int64_t)slot * 524288;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int col = col0 + 16 * j;
+        float s[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w, s1[j].x, s1[j].y, s1[j].z, s1[j].w};
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            s[e] = s[e] * decay;
+            part = fmaf(s[e], in.k[e], part);
+        }
+        const float dot_sk = row16_sum(part);
+        const float delta = (in.v[j] - dot_sk) * in.beta;
+        float att = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            s[e] = fmaf(in.k[e], delta, s[e]);
+            att = fmaf(s[e], in.q[e], att);
+        }
+        const float y = row16_sum(att);
+        if (li == 0) out[((int64_t)t * 32 + h) * 128 + col] = y * a.scale;
+        s0[j] = make_float4(s[0], s[1], s[2], s[3]);
+        s1[j] = make_float4(s[4], s[5], s[6], s[7]);
+        if (keep) {
+            float* snap = out + s_off + slot_off + ((int64_t)h * 128 + col) * 128;
+            *(float4*)(snap + 4 * li) = s0[j];
+            *(float4*)(snap + 64 + 4 * li) = s1[j];
+        }
+    }
+}
+
+// CPT state columns per 16-lane row. The state loads are all issued at the
+// start. ONE (a single token, the decode step) has no prefetch; otherwise each
+// token's inputs are loaded while the previous token computes, into two
+// alternating buffers, so that every load is issued ahead of the previous
+// token's stores (on gfx9 a wait for a load also waits for the stores issued
+// before it).
+template <bool BF16, bool VEC, int CPT, bool ONE>
 __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
     constexpr int COLS = 16 * CPT;  // columns per workgroup
     const int n_wg = a.B * 32 * (128 / COLS);
@@ -90,71 +150,35 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
         s0[j] = *(const float4*)(sc + 4 * li);
         s1[j] = *(const float4*)(sc + 64 + 4 * li);
     }
-
     float* out = (float*)((char*)a.dst + (int64_t)b * a.dst_nb2);
-    const int64_t s_off = (int64_t)4096 * a.T;
-
-    for (int t = 0; t < a.T; ++t) {
-        const uint8_t* qp = a.q + (int64_t)b * a.q_nb3 + (int64_t)t * a.q_nb2 + (int64_t)kh * a.q_nb1;
-        const uint8_t* kp = a.k + (int64_t)b * a.k_nb3 + (int64_t)t * a.k_nb2 + (int64_t)kh * a.k_nb1;
-        float qv[8], kv[8];
-        ld_row8<BF16, VEC>(qp, li, qv);
-        ld_row8<BF16, VEC>(kp, li, kv);
-        const float gt = *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)t * a.g_nb2 + (int64_t)h * a.g_nb1);
-        const float bt = *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)t * a.b_nb2 + (int64_t)h * a.b_nb1);
-        const uint8_t* vrow = a.v + (int64_t)b * a.v_nb3 + (int64_t)t * a.v_nb2 + (int64_t)h * a.v_nb1;
-        const float decay = expf(gt);
-        const int slot = a.T - 1 - t;
-        const bool keep = (a.slots > 1 && slot < a.slots) || (a.slots == 1 && t + 1 == a.T);
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int col = col0 + 16 * j;
-            const float vt = ld_elem<BF16>(vrow, col);
-            float s[8] = {s0[j].x, s0[j].y, s0[j].z, s0[j].w, s1[j].x, s1[j].y, s1[j].z, s1[j].w};
-            float part = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                s[e] = s[e] * decay;
-                part = fmaf(s[e], kv[e], part);
-            }
-            const float dot_sk = row16_sum(part);
-            const float delta = (vt - dot_sk) * bt;
-            float att = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                s[e] = fmaf(kv[e], delta, s[e]);
-                att = fmaf(s[e], qv[e], att);
-            }
-            const float y = row16_sum(att);
-            if (li == 0) out[((int64_t)t * 32 + h) * 128 + col] = y * a.scale;
-            s0[j] = make_float4(s[0], s[1], s[2], s[3]);
-            s1[j] = make_float4(s[4], s[5], s[6], s[7]);
-            if (keep) {
-                float* snap = out + s_off + (int64_t)(a.slots == 1 ? 0 : slot) * 524288 + ((int64_t)h * 128 + col) * 128;
-                *(float4*)(snap + 4 * li) = s0[j];
-                *(float4*)(snap + 64 + 4 * li) = s1[j];
-            }
+    StepIn<CPT> ia;
+    load_token<BF16, VEC, CPT>(a, b, h, kh, li, col0, 0, ia);
+    if constexpr (ONE) {
+        step_token<CPT, true>(a, ia, s0, s1, out, h, li, col0, 0);
+    } else {
+        StepIn<CPT> ib;
+        for (int t = 0; t < a.T; t += 2) {
+            if (t + 1 < a.T) load_token<BF16, VEC, CPT>(a, b, h, kh, li, col0, t + 1, ib);
+            step_token<CPT, false>(a, ia, s0, s1, out, h, li, col0, t);
+            if (t + 1 >= a.T) break;
+            if (t + 2 < a.T) load_token<BF16, VEC, CPT>(a, b, h, kh, li, col0, t + 2, ia);
+            step_token<CPT, false>(a, ib, s0, s1, out, h, li, col0, t + 1);
         }
     }
 }
 
-template <bool BF16, bool VEC>
-static void gdn_step_dispatch(int cpt, int B, hipStream_t stream, const GdnStepArgs& a) {
-    switch (cpt) {
-    case 1: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 1>), dim3(B * 32 * 8), dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 2>), dim3(B * 32 * 4), dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 4>), dim3(B * 32 * 2), dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, 8>), dim3(B * 32 * 1), dim3(256), 0, stream, a); break;
-    }
-}
+// Four columns per row: 64 columns (32 KB of state) per workgroup, two
+// workgroups per (sequence, v-head). Measured against one, two and eight
+// columns per row at 8 sequences x 32 heads, four was fastest.
+constexpr int kStepCpt = 4;
 
-static int gdn_cpt() {
-    static int cpt = [] {
-        const char* e = getenv("XQ_GDN_CPT");
-        const int v = e ? atoi(e) : 2;
-        return (v == 1 || v == 2 || v == 4 || v == 8) ? v : 2;
-    }();
-    return cpt;
+template <bool BF16, bool VEC>
+static void step_dispatch(const GdnStepArgs& a, hipStream_t stream) {
+    const dim3 grid(a.B * 32 * (128 / (16 * kStepCpt)));
+    if (a.T == 1)
+        hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, kStepCpt, true>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, kStepCpt, false>), grid, dim3(256), 0, stream, a);
 }
 
 hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
@@ -184,14 +208,13 @@ hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
         vec = vec && ((uintptr_t)t->data % al == 0);
         for (int i = 1; i < 4; ++i) vec = vec && (t->nb[i] % al == 0);
     }
-    const int cpt = gdn_cpt();
     ProfScope ps("gdn_step", stream);
     if (bf16) {
-        if (vec) gdn_step_dispatch<true, true>(cpt, a.B, stream, a);
-        else gdn_step_dispatch<true, false>(cpt, a.B, stream, a);
+        if (vec) step_dispatch<true, true>(a, stream);
+        else step_dispatch<true, false>(a, stream);
     } else {
-        if (vec) gdn_step_dispatch<false, true>(cpt, a.B, stream, a);
-        else gdn_step_dispatch<false, false>(cpt, a.B, stream, a);
+        if (vec) step_dispatch<false, true>(a, stream);
+        else step_dispatch<false, false>(a, stream);
     }
     return hipGetLastError();
 }
