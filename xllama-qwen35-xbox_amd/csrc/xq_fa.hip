@@ -788,7 +788,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
         a.part_ml = (float2*)(ws + off);
     }
 
-    const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G);
+    const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G) && fa_mma_mask_ok(a);
     if (L.engine == XQ_FA_ENGINE_MFMA && !mma) return hipErrorInvalidValue;
     if (mma) return fa_mma_launch(a, L, stream);
     Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);

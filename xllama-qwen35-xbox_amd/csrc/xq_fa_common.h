@@ -56,7 +56,6 @@ struct FaArgs {
     int64_t q_nb1, q_nb2, q_nb3;
     int32_t hi_only;
     int32_t fused_merge;
-    int32_t mask_vec;  // mask rows readable as 8-byte groups at every slice start
 };
 
 XQ_DEV float alibi_slope(const FaArgs& a, int h) {
@@ -96,6 +95,8 @@ XQ_DEV uint32_t lds_u16(const uint8_t* p) { return *(const uint16_t*)p; }
 
 struct FaLaunch;
 hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream);
+// Mask layout the matrix-core engine can read (4-byte aligned rows).
+bool fa_mma_mask_ok(const FaArgs& a);
 // Separate split-merge kernel (used when the merge cannot run inside pass 1).
 hipError_t fa_reduce_launch(const FaArgs& a, int d, hipStream_t stream);
 

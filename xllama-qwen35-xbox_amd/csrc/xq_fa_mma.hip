@@ -61,6 +61,8 @@ constexpr float kPOff = 4.0f;          // weights are exp2(x - max - 4), in (0, 
 // Arrival counters of the in-kernel split merge; zero at load, and every
 // completed group leaves its counter at zero again.
 __device__ uint32_t g_fa_arrivals[kMaxGroups];
+// Mask source of calls without a mask: one zero f16 pair.
+__device__ uint32_t g_fa_zero_mask[1];
 
 template <int KT, int D, int MT>
 struct DecCfg {
@@ -74,11 +76,16 @@ struct DecCfg {
     static constexpr bool QUANT = is_quant(KT);
     static constexpr int QRB = QUANT ? D + 8 * NB : 0;      // LDS Q image row bytes (int8 path)
     static constexpr int RING_W = 2 * 2 * SLICE;            // per wave: 2 stages x (K, V)
-    static constexpr bool NW8 = 8 * RING_W + NPP * QRB <= 144 * 1024 && !(MT == 2 && D == 256);
+    static constexpr int MASK_W = 2 * MT * 512;             // per wave: 2 stages x MT x 2 f16 pairs per lane
+    static constexpr int FIXED = NPP * QRB + 2 * 8 * NPP * 4 + 64;
+    static constexpr bool NW8 = 8 * (RING_W + MASK_W) + FIXED <= 160 * 1024 && !(MT == 2 && D == 256);
     static constexpr int NW = NW8 ? 8 : 4;
     static constexpr int RING = NW * RING_W;
+    static constexpr int QIMG = RING;                       // Q image after the K/V rings
+    static constexpr int MASKR = QIMG + NPP * QRB;          // mask rings after the Q image
     static constexpr int MERGE = NW * 16 * D * 4;
-    static constexpr int SMEM = RING + NPP * QRB > MERGE ? RING + NPP * QRB : MERGE;
+    static constexpr int LOOP = MASKR + NW * MASK_W;
+    static constexpr int SMEM = LOOP > MERGE ? LOOP : MERGE;
     static constexpr bool FITS = SMEM + 2 * NW * NPP * 4 + 64 <= 160 * 1024;
 };
 
@@ -133,13 +140,27 @@ XQ_DEV float xrow_sum(float x) {
     return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
-// HBM -> LDS without registers: lane l's CS bytes land at lds + l*CS.
+// HBM -> LDS without registers: lane l's CS bytes from base + off land at
+// lds + l*CS (m0 = the LDS address of lane 0). Written as inline assembly so
+// the compiler's wait insertion, which cannot tell the ring stages apart and
+// would wait for every DMA in flight before any ring read, adds no waits: the
+// kernel's explicit vmcnt waits order each DMA group before the reads of its
+// stage, and the asm's memory clobber keeps LDS reads on their side of them.
+// One wait state separates the m0 write from its use by the DMA.
 template <int CS>
-XQ_DEV void lds_dma(const uint8_t* g, uint8_t* lds) {
+XQ_DEV void lds_dma(const uint8_t* base, uint32_t off, uint8_t* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     if constexpr (CS == 16)
-        __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
     else
-        __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
+}
+// Same with a per-lane 64-bit address (4 bytes per lane).
+XQ_DEV void lds_dma4_ptr(const void* g, uint8_t* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 
 // Head dim held by accumulator register i of value tile (block c, half t) in
@@ -150,7 +171,7 @@ XQ_DEV int acc_dim(int c, int t, int lg, int i) {
     return KT == XQ_TYPE_Q4_0 ? 32 * c + 16 * t + 4 * lg + i : 32 * c + 8 * lg + 2 * i + t;
 }
 
-template <int KT, int D, int MT>
+template <int KT, int D, int MT, bool SOFTCAP, bool HI_ONLY>
 __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a) {
     using C = DecCfg<KT, D, MT>;
     constexpr int REC = C::REC, SLICE = C::SLICE, CS = C::CS, CPS = C::CPS, NIS = C::NIS;
@@ -183,20 +204,18 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     const int lr = lane & 15;
     const int lg = lane >> 4;
 
-    // ---- rows of this split; with positions each pair sees rows < its causal limit
-    const int64_t r0 = (int64_t)split * a.split_rows;
-    int64_t r_end = min(a.L, r0 + a.split_rows);
-    int64_t r_all = r_end;  // rows below every valid pair's limit
+    // ---- rows of this split (row indices are 32-bit: the host keeps L below
+    //      2^30); with positions each pair sees rows below its causal limit
+    const int r0 = split * (int)a.split_rows;
+    int r_end = (int)min(a.L, (int64_t)r0 + a.split_rows);
     if (a.positions) {
-        int64_t lmax = 0, lmin = a.L;
+        int lmax = 0;
         for (int qq = 0; qq < nqt; ++qq) {
             const int32_t pos = a.positions[iq0 + qq];
-            const int64_t lim = min(a.L, pos < a.origin ? (int64_t)0 : (int64_t)pos - a.origin + 1);
+            const int lim = pos < a.origin ? 0 : (int)min(a.L, (int64_t)pos - a.origin + 1);
             lmax = max(lmax, lim);
-            lmin = min(lmin, lim);
         }
         r_end = min(r_end, lmax);
-        r_all = min(r_end, lmin);
     }
     const uint8_t* kb = a.k + (int64_t)(b / a.rk3) * a.k_nb3 + (int64_t)g_kv * a.k_nb2;
     const uint8_t* vb = a.v + (int64_t)(b / a.rv3) * a.v_nb3 + (int64_t)g_kv * a.v_nb2;
@@ -214,34 +233,40 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         vo[i] = (uint32_t)(crow[i] * a.v_nb1 + (c % (REC / CS)) * CS);
     }
     // one group = NIS K loads then NIS V loads (exactly 2 * NIS vector-memory
-    // instructions), then the mask loads of the slice
-    auto stage = [&](int64_t t0, int st) {
-        const uint8_t* kt = kb + t0 * a.k_nb1;
-        const uint8_t* vt = vb + t0 * a.v_nb1;
+    // instructions), then the mask loads of the slice. A whole slice reads
+    // constant per-lane offsets from a wave-uniform row base; in the slice that
+    // holds the last live row, the rows past it re-read that row.
+    auto stage = [&](int t0, int st) {
+        const uint8_t* kt = kb + (int64_t)t0 * a.k_nb1;
+        const uint8_t* vt = vb + (int64_t)t0 * a.v_nb1;
         uint8_t* lk = ring + st * 2 * SLICE;
         uint8_t* lv = lk + SLICE;
-        const bool full = t0 + kSub <= r_end;
+        if (t0 + kSub <= r_end) {
 #pragma unroll
-        for (int i = 0; i < NIS; ++i) {
-            uint32_t kof = ko[i], vof = vo[i];
-            if (!full && t0 + crow[i] >= r_end) {  // rows past the end re-read the last live row
-                const uint32_t dr = (uint32_t)(t0 + crow[i] - (r_end - 1));
-                kof -= dr * (uint32_t)a.k_nb1;
-                vof -= dr * (uint32_t)a.v_nb1;
+            for (int i = 0; i < NIS; ++i)
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(kt, ko[i], lk + i * 64 * CS);
+#pragma unroll
+            for (int i = 0; i < NIS; ++i)
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(vt, vo[i], lv + i * 64 * CS);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NIS; ++i) {
+                const uint32_t dr = t0 + crow[i] >= r_end ? (uint32_t)(t0 + crow[i] - (r_end - 1)) : 0u;
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64)
+                    lds_dma<CS>(kt, ko[i] - dr * (uint32_t)a.k_nb1, lk + i * 64 * CS);
             }
-            if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(kt + kof, lk + i * 64 * CS);
-        }
 #pragma unroll
-        for (int i = 0; i < NIS; ++i) {
-            uint32_t vof = vo[i];
-            if (!full && t0 + crow[i] >= r_end) vof -= (uint32_t)(t0 + crow[i] - (r_end - 1)) * (uint32_t)a.v_nb1;
-            if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(vt + vof, lv + i * 64 * CS);
+            for (int i = 0; i < NIS; ++i) {
+                const uint32_t dr = t0 + crow[i] >= r_end ? (uint32_t)(t0 + crow[i] - (r_end - 1)) : 0u;
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64)
+                    lds_dma<CS>(vt, vo[i] - dr * (uint32_t)a.v_nb1, lv + i * 64 * CS);
+            }
         }
     };
 
     // ---- per-pair state of this lane's pairs 16m + lr (identical in the four lane groups)
     float m_run[MT], l_run[MT], slope2[MT];
-    int64_t lim[MT];
+    int lim[MT];
     const uint16_t* mrow[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -256,64 +281,48 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             lim[m] = r_end;
             if (a.positions) {
                 const int32_t pos = a.positions[iq0 + qq];
-                lim[m] = min(r_end, pos < a.origin ? (int64_t)0 : (int64_t)pos - a.origin + 1);
+                lim[m] = pos < a.origin ? 0 : (int)min((int64_t)r_end, (int64_t)pos - a.origin + 1);
             }
             slope2[m] = alibi_slope(a, h) * kLog2e;
         }
-        // padding pairs read the first pair's mask row (always valid memory)
+        // padding pairs read the first pair's mask row (always valid memory); with
+        // no mask every pair reads the first f16 pair of a zero row
         mrow[m] = a.mask ? (const uint16_t*)(a.mask + (int64_t)(iq0 + qq) * a.m_nb1 + (int64_t)(h % a.m_ne2) * a.m_nb2 +
                                              (int64_t)(b % a.m_ne3) * a.m_nb3)
-                         : nullptr;
+                         : (const uint16_t*)g_fa_zero_mask;
     }
-    // additive mask of a slice as f16 pairs (rows 4lg + 0,1 and 4lg + 2,3), with
-    // -inf for rows past the pair's limit
-    auto load_mask = [&](int64_t t, uint32_t (&mk)[MT][2]) {
-        const int64_t r = t + 4 * lg;
-        if (t + kSub <= r_all) {
+    // mask of a slice: lane (lr, lg) brings rows t + 4lg + 2k, +1 (k = 0, 1) of its
+    // pair's mask row as one f16 pair into its slot of the wave's mask ring, in the
+    // same DMA group as K and V, so the loop holds no register-destination loads.
+    // Rows at or past the mask's end read the row's first pair (they lie past every
+    // pair's limit and are replaced by -inf); the pair at the last row, when L is
+    // odd, reads the aligned dword that holds it (the host requires 4-byte aligned
+    // mask rows).
+    const int mcols = a.mask ? (int)a.L : 0;
+    uint8_t* mring = smem + C::MASKR + wave * C::MASK_W;
+    auto load_mask = [&](int t, int st) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (!a.mask) {
-                    mk[m][0] = mk[m][1] = 0;
-                } else if (a.mask_vec) {
-                    const uint2 w = *(const uint2*)(mrow[m] + r);
-                    mk[m][0] = w.x;
-                    mk[m][1] = w.y;
-                } else {
-                    mk[m][0] = (uint32_t)mrow[m][r] | ((uint32_t)mrow[m][r + 1] << 16);
-                    mk[m][1] = (uint32_t)mrow[m][r + 2] | ((uint32_t)mrow[m][r + 3] << 16);
-                }
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int r = t + 4 * lg + 2 * k;
+                lds_dma4_ptr(mrow[m] + (r < mcols ? r : 0), mring + (st * MT + m) * 512 + k * 256);
             }
-        } else {
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                uint32_t v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = r + i < lim[m] ? (a.mask ? (uint32_t)mrow[m][r + i] : 0u) : 0xfc00u;
-                mk[m][0] = v[0] | (v[1] << 16);
-                mk[m][1] = v[2] | (v[3] << 16);
-            }
-        }
     };
 
-    const int64_t step = (int64_t)kSub * NW;
-    int64_t t0 = r0 + kSub * wave;
-    uint32_t mk[2][MT][2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) mk[s2][m][0] = mk[s2][m][1] = kNegInfH2;
+    const int step = kSub * NW;
+    int t0 = r0 + kSub * wave;
     // both ring stages in flight before the Q image is built
     if (t0 < r_end) {
         stage(t0, 0);
-        load_mask(t0, mk[0]);
+        load_mask(t0, 0);
     }
     if (t0 + step < r_end) {
         stage(t0 + step, 1);
-        load_mask(t0 + step, mk[1]);
+        load_mask(t0 + step, 1);
     }
-
     // ---- int8 Q image of the tile's pairs in LDS (pairs >= npa are zero)
-    uint8_t* sQ = smem + C::RING;
+    uint8_t* sQ = smem + C::QIMG;
     if constexpr (QUANT) {
         constexpr int VD = D / 64;
         constexpr int LPB = kQK / VD;
@@ -401,7 +410,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     const float xv = src ? src[32 * c + 8 * lg + j] : 0.0f;
                     const uint32_t hb = f32_to_f16_bits(xv);
                     qh[m][c][j] = __builtin_bit_cast(_Float16, (uint16_t)hb);
-                    ql[m][c][j] = a.hi_only ? (_Float16)0.0f
+                    ql[m][c][j] = HI_ONLY ? (_Float16)0.0f
                                             : __builtin_bit_cast(_Float16, (uint16_t)f32_to_f16_bits(xv - f16_bits_to_f32(hb)));
                 }
             }
@@ -417,12 +426,12 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         for (int n = 0; n < 2 * NB; ++n) acc[m][n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // ---- one 16-row slice from ring stage S (S static: the loop is unrolled by two)
-    auto slice = [&](int64_t t, auto stage_tag) {
+    auto slice = [&](int t, auto stage_tag) {
         constexpr int S = decltype(stage_tag)::value;
         // this slice's group is complete once at most one group (the next slice's,
-        // >= 2 * NIS instructions, issued later) is outstanding; loads return in order
+        // 2 * NIS + 2 * MT instructions, issued later) is outstanding; loads return in order
         if (t + step < r_end)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS) : "memory");
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
@@ -436,25 +445,37 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[m][i] = 0.0f;
+            // blocks in batches: the batch's operand reads, then its independent
+            // MFMAs, then the block-scale arithmetic of the batch
+            constexpr int CB = MT == 1 ? 4 : 2;
 #pragma unroll
-            for (int c = 0; c < NB; ++c) {
-                const int64_t ka = k_block_bytes<KT>(Ks + lr * REC, c, lg);
-                uint32_t dkw[4];  // K scales of rows 4lg + i (low or high half)
+            for (int c0 = 0; c0 < NB; c0 += CB) {
+                int64_t ka[CB];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) dkw[i] = lds_u32(Ks + (4 * lg + i) * REC + ((BB * c) & ~3));
-                const bool dhi = ((BB * c) & 2) != 0;
+                for (int j = 0; j < CB; ++j) ka[j] = k_block_bytes<KT>(Ks + lr * REC, c0 + j, lg);
+                i4 I[MT][CB];
 #pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const i4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka, qb[m][c], i4{0, 0, 0, 0}, 0, 0, 0);
+                for (int j = 0; j < CB; ++j)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        float tv = (float)I[i];
-                        if constexpr (KT == XQ_TYPE_Q4_0)
-                            tv = fmaf(tv, dq[m][c], qcorr[m][c]);
-                        else
-                            tv = tv * dq[m][c];
-                        const h2 dh = __builtin_bit_cast(h2, dkw[i]);
-                        s[m][i] = fmaf(tv, dhi ? (float)dh[1] : (float)dh[0], s[m][i]);
+                    for (int m = 0; m < MT; ++m)
+                        I[m][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka[j], qb[m][c0 + j], i4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < CB; ++j) {
+                    const int c = c0 + j;
+                    _Float16 dk[4];  // K scales of rows 4lg + i
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dk[i] = *(const _Float16*)(Ks + (4 * lg + i) * REC + BB * c);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float tv = (float)I[m][j][i];
+                            if constexpr (KT == XQ_TYPE_Q4_0)
+                                tv = fmaf(tv, dq[m][c], qcorr[m][c]);
+                            else
+                                tv = tv * dq[m][c];
+                            s[m][i] = fmaf(tv, (float)dk[i], s[m][i]);
+                        }
                     }
                 }
             }
@@ -476,7 +497,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[m][c], sc[m], 0, 0, 0);
-                    if (!a.hi_only) sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[m][c], sc[m], 0, 0, 0);
+                    if (!HI_ONLY) sc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[m][c], sc[m], 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -485,17 +506,20 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 for (int i = 0; i < 4; ++i) s[m][i] = sc[m][i];
         }
 
-        // -- online softmax (base 2); the mask pairs carry -inf for invalid rows
+        // -- online softmax (base 2); rows past a pair's limit are -inf
         float x[MT][4];
         bool grow = false;
         float mnew[MT];
+        const uint8_t* ms = mring + S * MT * 512 + 4 * lane;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
+            const uint32_t mw[2] = {lds_u32(ms + m * 512), lds_u32(ms + m * 512 + 256)};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const h2 mh = __builtin_bit_cast(h2, mk[S][m][i >> 1]);
-                const float v = a.softcap != 0.0f ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
-                x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
+                const h2 mh = __builtin_bit_cast(h2, mw[i >> 1]);
+                const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
+                const float xv = fmaf(slope2[m], (float)mh[i & 1], v);
+                x[m][i] = t + 4 * lg + i < lim[m] ? xv : -INFINITY;
             }
             const float mt = xrow_max(fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3])));
             mnew[m] = mt > m_run[m] + kLazyMax ? mt : m_run[m];
@@ -522,7 +546,6 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             P[m][0] = h2{(_Float16)p[0], (_Float16)p[1]};
             P[m][1] = h2{(_Float16)p[2], (_Float16)p[3]};
         }
-
         // -- values: acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x P^T
 #pragma unroll
         for (int c = 0; c < NB; ++c) {
@@ -588,11 +611,11 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         }
 
         // -- refill this stage with the slice two steps ahead
-        const int64_t tr = t + 2 * step;
+        const int tr = t + 2 * step;
         if (tr < r_end) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage done
             stage(tr, S);
-            load_mask(tr, mk[S]);
+            load_mask(tr, S);
         }
     };
     for (; t0 < r_end; t0 += 2 * step) {
@@ -749,17 +772,25 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 
 using DecFn = void (*)(FaArgs);
 
+// Variant of (type, head dim, pair tiles) for the call's softcap and Q policy
+// (hi-only f16 Q exists for float K only).
 template <int KT, int D, int MT>
-static DecFn dec_inst() {
-    if constexpr (DecCfg<KT, D, MT>::FITS)
-        return fa_dec<KT, D, MT>;
-    else
+static DecFn dec_inst(bool softcap, bool hi_only) {
+    if constexpr (DecCfg<KT, D, MT>::FITS) {
+        if constexpr (is_quant(KT)) {
+            return softcap ? fa_dec<KT, D, MT, true, false> : fa_dec<KT, D, MT, false, false>;
+        } else {
+            if (softcap) return hi_only ? fa_dec<KT, D, MT, true, true> : fa_dec<KT, D, MT, true, false>;
+            return hi_only ? fa_dec<KT, D, MT, false, true> : fa_dec<KT, D, MT, false, false>;
+        }
+    } else {
         return nullptr;
+    }
 }
 
 template <int KT, int D>
-static DecFn dec_for(int mt) {
-    return mt == 1 ? dec_inst<KT, D, 1>() : mt == 2 ? dec_inst<KT, D, 2>() : nullptr;
+static DecFn dec_for(int mt, bool softcap, bool hi_only) {
+    return mt == 1 ? dec_inst<KT, D, 1>(softcap, hi_only) : mt == 2 ? dec_inst<KT, D, 2>(softcap, hi_only) : nullptr;
 }
 
 template <int KT, int D>
@@ -767,22 +798,25 @@ static int waves_for(int mt) {
     return mt == 1 ? DecCfg<KT, D, 1>::NW : DecCfg<KT, D, 2>::NW;
 }
 
-static DecFn dec_lookup(int kt, int d, int mt, int* waves) {
+static DecFn dec_lookup(int kt, int d, int mt, int* waves, bool softcap = false, bool hi_only = false) {
+#define XQ_DEC_CASE(T, DD) \
+    case T: *waves = waves_for<T, DD>(mt); return dec_for<T, DD>(mt, softcap, hi_only);
     if (d == 128) {
         switch (kt) {
-        case XQ_TYPE_Q8_0: *waves = waves_for<XQ_TYPE_Q8_0, 128>(mt); return dec_for<XQ_TYPE_Q8_0, 128>(mt);
-        case XQ_TYPE_Q4_0: *waves = waves_for<XQ_TYPE_Q4_0, 128>(mt); return dec_for<XQ_TYPE_Q4_0, 128>(mt);
-        case XQ_TYPE_F16: *waves = waves_for<XQ_TYPE_F16, 128>(mt); return dec_for<XQ_TYPE_F16, 128>(mt);
-        case XQ_TYPE_E5M2: *waves = waves_for<XQ_TYPE_E5M2, 128>(mt); return dec_for<XQ_TYPE_E5M2, 128>(mt);
+            XQ_DEC_CASE(XQ_TYPE_Q8_0, 128)
+            XQ_DEC_CASE(XQ_TYPE_Q4_0, 128)
+            XQ_DEC_CASE(XQ_TYPE_F16, 128)
+            XQ_DEC_CASE(XQ_TYPE_E5M2, 128)
         }
     } else if (d == 256) {
         switch (kt) {
-        case XQ_TYPE_Q8_0: *waves = waves_for<XQ_TYPE_Q8_0, 256>(mt); return dec_for<XQ_TYPE_Q8_0, 256>(mt);
-        case XQ_TYPE_Q4_0: *waves = waves_for<XQ_TYPE_Q4_0, 256>(mt); return dec_for<XQ_TYPE_Q4_0, 256>(mt);
-        case XQ_TYPE_F16: *waves = waves_for<XQ_TYPE_F16, 256>(mt); return dec_for<XQ_TYPE_F16, 256>(mt);
-        case XQ_TYPE_E5M2: *waves = waves_for<XQ_TYPE_E5M2, 256>(mt); return dec_for<XQ_TYPE_E5M2, 256>(mt);
+            XQ_DEC_CASE(XQ_TYPE_Q8_0, 256)
+            XQ_DEC_CASE(XQ_TYPE_Q4_0, 256)
+            XQ_DEC_CASE(XQ_TYPE_F16, 256)
+            XQ_DEC_CASE(XQ_TYPE_E5M2, 256)
         }
     }
+#undef XQ_DEC_CASE
     return nullptr;
 }
 
@@ -799,6 +833,11 @@ int fa_mma_waves(int kt, int d, int n_pairs) {
     return w;
 }
 
+// The mask rows are read as 4-byte pairs: every row base must be 4-byte aligned.
+bool fa_mma_mask_ok(const FaArgs& a) {
+    return !a.mask || ((uintptr_t)a.mask % 4 == 0 && a.m_nb1 % 4 == 0 && a.m_nb2 % 4 == 0 && a.m_nb3 % 4 == 0);
+}
+
 bool fa_mma_fused_merge(int64_t n_groups, int n_pairs, int n_splits) {
     return n_splits > 1 && n_groups <= kMaxGroups && (int64_t)n_pairs * n_splits <= kFusedMergeMax;
 }
@@ -807,20 +846,18 @@ hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
     const int D = (int)L.q->ne[0];
     const int kt = L.k->type;
     const int mt = (a.QT * a.G + 15) / 16;
+    if (a.L >= (int64_t)1 << 30) return hipErrorInvalidValue;  // 32-bit row indices
+    a.hi_only = is_quant(kt) ? 0 : (L.q_round_f16 ? 1 : 0);
     int waves = 0;
-    DecFn fn = dec_lookup(kt, D, mt, &waves);
+    DecFn fn = dec_lookup(kt, D, mt, &waves, a.softcap != 0.0f, a.hi_only != 0);
     if (!fn) return hipErrorInvalidValue;
     a.q = (const uint8_t*)L.q->data;
     a.q_nb1 = (int64_t)L.q->nb[1];
     a.q_nb2 = (int64_t)L.q->nb[2];
     a.q_nb3 = (int64_t)L.q->nb[3];
-    a.hi_only = is_quant(kt) ? 0 : (L.q_round_f16 ? 1 : 0);
     const int64_t n_groups = (int64_t)a.B * a.Hkv * a.n_qtiles;
     a.fused_merge = fa_mma_fused_merge(n_groups, a.QT * a.G, a.n_splits) ? 1 : 0;
-    // 4-row mask groups start at multiples of 4 rows; 8-byte reads need every
-    // row base 8-byte aligned
-    a.mask_vec = a.mask && ((uintptr_t)a.mask % 8) == 0 && a.m_nb1 % 8 == 0 && a.m_nb2 % 8 == 0 &&
-                 a.m_nb3 % 8 == 0 && a.split_rows % 4 == 0;
+    if (!fa_mma_mask_ok(a)) return hipErrorInvalidValue;
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     {
         ProfScope ps("fa_dec", stream);
