@@ -21,11 +21,9 @@
  * whose size is returned by the *_workspace queries. Errors are returned as
  * xq_status codes (never abort); xq_last_error() gives a message for the
  * calling thread. Calls sharing one workspace buffer must be ordered by the
- * caller. xq_flash_attn_ext calls with more than one KV split merge their
- * splits inside the kernel through an arrival-counter array the library keeps
- * per device (zero at load, left at zero by every completed call): two such
- * calls must not run concurrently on one device (calls on one stream, or
- * inside one captured graph, are ordered and safe).
+ * caller. xq_flash_attn_ext calls with more than one KV split launch a second
+ * kernel (the ascending-order split merge) on the same stream; calls keep no
+ * state between them.
  */
 #ifndef XQ_ATTN_H
 #define XQ_ATTN_H

@@ -484,14 +484,20 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
 template <int D>
 __global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
     __shared__ float sm[kMaxSplits], sl[kMaxSplits], sw[kMaxSplits];
-    __shared__ float sA1, sInv, sMax[D / 64];
-    __shared__ int sBad;
+    __shared__ float sMax[D / 64];
     const int64_t row = blockIdx.x;
     const int S = a.n_splits;
     const int d = threadIdx.x;
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
     const int b = (int)(row / rows_per_seq);
     const int h = (int)(row % a.H);
+    // the numerators of the first CH splits are loaded together with the split
+    // states: one memory round trip for S <= CH
+    constexpr int CH = 16;
+    const float* po = a.part_o + row * S * D + d;
+    float v0[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) v0[i] = i < S ? po[(int64_t)i * D] : 0.0f;
     float mloc = -3.402823466e38f;
     int bad = 0;
     for (int s = d; s < S; s += D) {
@@ -513,24 +519,20 @@ __global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
     for (int w = 1; w < D / 64; ++w) M = fmaxf(M, sMax[w]);
     for (int s = d; s < S; s += D) sw[s] = sl[s] != 0.0f ? expf(sm[s] - M) : 0.0f;
     __syncthreads();
-    if (d == 0) {
-        float L = 0.0f;
-        for (int s = 0; s < S; ++s)
-            if (sl[s] != 0.0f) L = fmaf(sl[s], sw[s], L);
-        int badl = bad || !isfinite(L);
-        float a1, inv, lse;
-        fa_finalize(L == 0.0f ? -INFINITY : M, L, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
-        if (!isfinite(inv) || (L != 0.0f && !isfinite(lse))) badl = 1;
-        sA1 = a1;
-        sInv = inv;
-        sBad = badl && a.poison;
-        if (a.lse) a.lse[row] = (badl && a.poison) ? NAN : lse;
-    }
-    __syncthreads();
-    const float* po = a.part_o + row * S * D + d;
+    // every thread forms L (ascending split order) and the output factors itself
+    float L = 0.0f;
+    for (int s = 0; s < S; ++s)
+        if (sl[s] != 0.0f) L = fmaf(sl[s], sw[s], L);
+    int badl = bad || !isfinite(L);
+    float a1, inv, lse;
+    fa_finalize(L == 0.0f ? -INFINITY : M, L, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
+    if (!isfinite(inv) || (L != 0.0f && !isfinite(lse))) badl = 1;
+    badl = badl && a.poison;
     float acc = 0.0f;
-    constexpr int CH = 16;
-    for (int s0 = 0; s0 < S; s0 += CH) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+        if (i < S && sl[i] != 0.0f) acc = fmaf(v0[i], sw[i], acc);
+    for (int s0 = CH; s0 < S; s0 += CH) {
         float v[CH];
 #pragma unroll
         for (int i = 0; i < CH; ++i) v[i] = (s0 + i < S) ? po[(int64_t)(s0 + i) * D] : 0.0f;
@@ -538,14 +540,15 @@ __global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
         for (int i = 0; i < CH; ++i)
             if (s0 + i < S && sl[s0 + i] != 0.0f) acc = fmaf(v[i], sw[s0 + i], acc);
     }
-    float out = (acc * sA1) * sInv;
+    float out = (acc * a1) * inv;
     if (a.poison) {
         // any non-finite participating state or numerator poisons the whole row
-        if (__syncthreads_or(sBad || !isfinite(out))) {
+        if (__syncthreads_or(badl || !isfinite(out))) {
             out = NAN;
-            if (d == 0 && a.lse) a.lse[row] = NAN;
+            lse = NAN;
         }
     }
+    if (d == 0 && a.lse) a.lse[row] = lse;
     const int iq = (int)((row % rows_per_seq) / a.H);
     float* o = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
     o[d] = out;

@@ -51,11 +51,10 @@ struct FaArgs {
     int32_t n_head_log2;
     int32_t poison;
     // matrix-core engine: f32 Q rows (quantised inside the kernel), hi-only
-    // f16 Q for the NATIVE policy, split merge inside the kernel
+    // f16 Q for the NATIVE policy
     const uint8_t* q;
     int64_t q_nb1, q_nb2, q_nb3;
     int32_t hi_only;
-    int32_t fused_merge;
 };
 
 XQ_DEV float alibi_slope(const FaArgs& a, int h) {

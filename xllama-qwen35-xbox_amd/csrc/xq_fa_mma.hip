@@ -1,18 +1,18 @@
 // xq_fa_mma.hip — FLASH_ATTN_EXT decode / short multi-query verify on the
-// gfx950 matrix cores, one kernel launch per call: Q quantisation, the KV
-// stream, the merge of the wave states and the merge of the KV splits all
-// happen inside it.
+// gfx950 matrix cores: Q quantisation, the KV stream and the merge of the wave
+// states happen in one kernel; with several KV splits the ascending-order split
+// merge runs as fa_reduce right after it on the same stream (one memory round
+// trip there costs less than the cross-XCD round trips a last-arriving
+// workgroup needs to merge inside this kernel: 64.4 against 70.4 us per call
+// on the 32k q8_0 decode, 21.4 against 28.8 us on the 4k f16 decode).
 //
 // Work decomposition. A workgroup owns one (sequence, KV head, query tile,
 // KV split). Its NW waves stream disjoint 16-row slices of the split (slice j
 // goes to wave j % NW) through private double-buffered LDS rings filled by
 // global_load_lds, each with its own online softmax and no workgroup barrier
-// in the row loop. The wave states are merged through LDS at the end. With
+// in the row loop. The wave states are merged through LDS at the end; with
 // several splits each workgroup writes a partial state (unnormalised output,
-// running maximum, running sum) and the last workgroup of its (sequence, KV
-// head, query tile) group to arrive merges every split in ascending split
-// order; arrivals are counted in a device array that each completed group
-// returns to zero (atomicInc wrap-around).
+// running maximum, running sum) for fa_reduce.
 //
 // Products (M x N x K of each MFMA):
 //   scores  S = K Q^T, A = 16 KV rows, B = 16 (query, head) pairs.
@@ -20,7 +20,8 @@
 //           exact integer block dot of ggml's vec_dot_q8_0_q8_0 /
 //           vec_dot_q4_0_q8_0 between the K block and the q8_0-quantised Q
 //           row (q4_0 nibbles enter unsigned and 8*sum(q) is removed), then
-//           scaled by d_q and d_k in f32.
+//           scaled by d_k * d_q (one 4-block v_mfma_f32_16x16x1f32 forms the
+//           products of four blocks in the score layout) in f32.
 //           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exact f16 K with Q
 //           split into f16 hi + lo parts (the NATIVE policy uses hi alone).
 //   values  O^T = V^T P^T through v_mfma_f32_16x16x16_f16, A = 16 head dims,
@@ -29,9 +30,10 @@
 //           exactly the B operand layout of this product, so the softmax
 //           weights never leave registers and every per-pair quantity
 //           (maximum, sum, rescale factor) is lane-local. V is gathered from
-//           LDS per (row, dim) and converted exactly (int8 and q4_0 nibbles
-//           through the 0x6400 exponent trick, E5M2 by a byte shift); the V
-//           block scale multiplies the weights in f16.
+//           LDS per (row, dim) and converted exactly (int8 by SDWA sign-
+//           extending f16 conversions, q4_0 nibbles through the 0x6400
+//           exponent trick, E5M2 by a byte shift); the V block scale
+//           multiplies the weights in f16.
 // Online softmax in base 2 (scores pre-multiplied by log2 e) with a lazy
 // maximum: the running maximum moves only when a slice exceeds it by more
 // than 8, so accumulator rescales are rare; weights are taken relative to the
@@ -47,20 +49,16 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr bool is_quant(int kt) { return kt == XQ_TYPE_Q8_0 || kt == XQ_TYPE_Q4_0; }
 
 constexpr int kSub = 16;               // KV rows per wave slice
-constexpr int kMaxGroups = 16384;      // arrival counters (sequence x KV head x query tile)
-constexpr int kFusedMergeMax = 4096;   // pairs x splits merged inside the kernel
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazyMax = 8.0f;       // base-2 headroom before the running maximum moves
 constexpr float kPOff = 4.0f;          // weights are exp2(x - max - 4), in (0, 16]
 
-// Arrival counters of the in-kernel split merge; zero at load, and every
-// completed group leaves its counter at zero again.
-__device__ uint32_t g_fa_arrivals[kMaxGroups];
 // Mask source of calls without a mask: one zero f16 pair.
 __device__ uint32_t g_fa_zero_mask[1];
 
@@ -114,15 +112,24 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
 
-// f16 pair (signed byte t of a, signed byte t of b), exact: v_perm places the
-// two bytes in the low bytes of the two halves (high bytes zero); one XOR
-// flips the sign bit and sets the 0x64 exponent byte, giving f16 1152 + q;
-// a packed add of -1152 leaves q.
-template <int T>
-XQ_DEV uint32_t i8x2_f16(uint32_t a, uint32_t b) {
-    const uint32_t y = __builtin_amdgcn_perm(b, a, T == 0 ? 0x0c040c00u : 0x0c050c01u) ^ 0x64806480u;
-    const h2 v = __builtin_bit_cast(h2, y) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f};
-    return __builtin_bit_cast(uint32_t, v);
+// V^T operands of one q8_0 block: the signed bytes 0 (tile 0) and 1 (tile 1)
+// of the rows' 16-bit words x0..x3 as f16 pairs (rows 0,1 and rows 2,3),
+// exact. Each pair is two SDWA conversions of sign-extended bytes, the second
+// writing the high half and keeping the low one. The trailing s_nop gives the
+// two wait states an MFMA reading a VGPR needs after a VALU wrote it (the
+// compiler's hazard tracking does not see into the asm).
+XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32_t (&A0)[2], uint32_t (&A1)[2]) {
+    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "s_nop 1"
+        : "=&v"(A0[0]), "=&v"(A0[1]), "=&v"(A1[0]), "=&v"(A1[1])
+        : "v"(x0), "v"(x1), "v"(x2), "v"(x3));
 }
 
 // Reductions over the four 16-lane rows (lanes l, l^16, l^32, l^48) by
@@ -183,7 +190,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::SMEM];
     __shared__ float sM[NW][NPP], sL[NW][NPP];
-    __shared__ int sLast;
+    __shared__ int sProg[NW];  // slices each wave has finished (issue-priority balancing)
 
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     uint32_t wg = xcd_remap(blockIdx.x, n_wg);
@@ -208,14 +215,17 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     //      2^30); with positions each pair sees rows below its causal limit
     const int r0 = split * (int)a.split_rows;
     int r_end = (int)min(a.L, (int64_t)r0 + a.split_rows);
+    int r_all = r_end;  // rows below every pair's limit (per-row limits apply past it)
     if (a.positions) {
-        int lmax = 0;
+        int lmax = 0, lmin = (int)a.L;
         for (int qq = 0; qq < nqt; ++qq) {
             const int32_t pos = a.positions[iq0 + qq];
             const int lim = pos < a.origin ? 0 : (int)min(a.L, (int64_t)pos - a.origin + 1);
             lmax = max(lmax, lim);
+            lmin = min(lmin, lim);
         }
         r_end = min(r_end, lmax);
+        r_all = min(r_end, lmin);
     }
     const uint8_t* kb = a.k + (int64_t)(b / a.rk3) * a.k_nb3 + (int64_t)g_kv * a.k_nb2;
     const uint8_t* vb = a.v + (int64_t)(b / a.rv3) * a.v_nb3 + (int64_t)g_kv * a.v_nb2;
@@ -232,34 +242,29 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         ko[i] = (uint32_t)(crow[i] * a.k_nb1 + (c % (REC / CS)) * CS);
         vo[i] = (uint32_t)(crow[i] * a.v_nb1 + (c % (REC / CS)) * CS);
     }
-    // one group = NIS K loads then NIS V loads (exactly 2 * NIS vector-memory
-    // instructions), then the mask loads of the slice. A whole slice reads
-    // constant per-lane offsets from a wave-uniform row base; in the slice that
-    // holds the last live row, the rows past it re-read that row.
-    auto stage = [&](int t0, int st) {
-        const uint8_t* kt = kb + (int64_t)t0 * a.k_nb1;
-        const uint8_t* vt = vb + (int64_t)t0 * a.v_nb1;
-        uint8_t* lk = ring + st * 2 * SLICE;
-        uint8_t* lv = lk + SLICE;
+    // The ring is refilled in half-slice units: the K unit of a slice (NIS K
+    // loads, then its 2*MT mask loads) and its V unit (NIS V loads), each
+    // exactly that many vector-memory instructions. A unit reads constant
+    // per-lane offsets from a wave-uniform row base; in the slice that holds the
+    // last live row, the rows past it re-read that row.
+    // (r_end >= 1 wherever a unit is issued.)
+    auto unit = [&](const uint8_t* base, int64_t nb1, const uint32_t (&off)[NIS], int t0, uint8_t* dst) {
         if (t0 + kSub <= r_end) {
+            const uint8_t* bt = base + (int64_t)t0 * nb1;
 #pragma unroll
             for (int i = 0; i < NIS; ++i)
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(kt, ko[i], lk + i * 64 * CS);
-#pragma unroll
-            for (int i = 0; i < NIS; ++i)
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(vt, vo[i], lv + i * 64 * CS);
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(bt, off[i], dst + i * 64 * CS);
         } else {
+            // rows from tr = min(t0, r_end - 1); lane rows clamp to r_end - 1, so
+            // every offset is non-negative and below 16 rows (the whole slice
+            // may lie past the end)
+            const int tr = min(t0, r_end - 1);
+            const uint8_t* bt = base + (int64_t)tr * nb1;
 #pragma unroll
             for (int i = 0; i < NIS; ++i) {
-                const uint32_t dr = t0 + crow[i] >= r_end ? (uint32_t)(t0 + crow[i] - (r_end - 1)) : 0u;
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64)
-                    lds_dma<CS>(kt, ko[i] - dr * (uint32_t)a.k_nb1, lk + i * 64 * CS);
-            }
-#pragma unroll
-            for (int i = 0; i < NIS; ++i) {
-                const uint32_t dr = t0 + crow[i] >= r_end ? (uint32_t)(t0 + crow[i] - (r_end - 1)) : 0u;
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64)
-                    lds_dma<CS>(vt, vo[i] - dr * (uint32_t)a.v_nb1, lv + i * 64 * CS);
+                const int row = min(t0 + crow[i], r_end - 1);
+                const uint32_t o = off[i] + (uint32_t)(row - tr - crow[i]) * (uint32_t)nb1;
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS>(bt, o, dst + i * 64 * CS);
             }
         }
     };
@@ -273,12 +278,11 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         m_run[m] = -INFINITY;
         l_run[m] = 0.0f;
         slope2[m] = kLog2e;
-        lim[m] = 0;  // padding pair: every row invalid
+        lim[m] = r_end;  // padding pairs (zero Q, never stored) run like valid ones
         const int p = 16 * m + lr;
         const bool ok = p < npa;
         const int qq = ok ? p / a.G : 0, h = g_kv * a.G + (ok ? p % a.G : 0);
         if (ok) {
-            lim[m] = r_end;
             if (a.positions) {
                 const int32_t pos = a.positions[iq0 + qq];
                 lim[m] = pos < a.origin ? 0 : (int)min((int64_t)r_end, (int64_t)pos - a.origin + 1);
@@ -312,33 +316,71 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 
     const int step = kSub * NW;
     int t0 = r0 + kSub * wave;
-    // both ring stages in flight before the Q image is built
-    if (t0 < r_end) {
-        stage(t0, 0);
-        load_mask(t0, 0);
-    }
-    if (t0 + step < r_end) {
-        stage(t0 + step, 1);
-        load_mask(t0 + step, 1);
-    }
-    // ---- int8 Q image of the tile's pairs in LDS (pairs >= npa are zero)
+    constexpr int VD = D / 64;
+    constexpr int PPW = (NPP + NW - 1) / NW;
+    // Units: K_j, mask_j, V_j, then the same for slice j+1 (the loop keeps this
+    // issue order).
+    auto k_unit = [&](int tt, int st) {
+        unit(kb, a.k_nb1, ko, tt, ring + st * 2 * SLICE);
+        load_mask(tt, st);
+    };
+    auto v_unit = [&](int tt, int st) { unit(vb, a.v_nb1, vo, tt, ring + st * 2 * SLICE + SLICE); };
+
+    // ---- int8 path: wave w quantizes pairs w, w + NW, ... (VD floats per lane)
+    //      into the Q image in LDS (pairs >= npa are zero). The Q rows come by
+    //      DMA into the wave's ring stage 1, ahead of stage 0's units, and are
+    //      waited for alone (loads complete in order), so Q does not wait behind
+    //      the ring; stage 1's units follow once the rows are read.
+    //      Float K: the f16 hi / lo B operands straight from Q, then the units.
+    constexpr bool QSTAGE = QUANT && PPW * D * 4 <= 2 * SLICE;
     uint8_t* sQ = smem + C::QIMG;
+    h8 qh[QUANT ? 1 : MT][QUANT ? 1 : NB], ql[QUANT ? 1 : MT][QUANT ? 1 : NB];
     if constexpr (QUANT) {
-        constexpr int VD = D / 64;
         constexpr int LPB = kQK / VD;
-        constexpr int PPW = (NPP + NW - 1) / NW;
         float x[PPW][VD];
+        if constexpr (QSTAGE) {
+            uint8_t* qst = ring + 2 * SLICE;
 #pragma unroll
-        for (int k = 0; k < PPW; ++k) {  // every load first
-            const int p = wave + k * NW;
-            const bool ok = p < npa;
-            const float* src = (const float*)a.q;
-            if (ok) {
-                const int qq = p / a.G, h = g_kv * a.G + p % a.G;
-                src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+            for (int k = 0; k < PPW; ++k) {
+                const int p = wave + k * NW;  // wave-uniform
+                if (p < npa) {
+                    const int qq = p / a.G, h = g_kv * a.G + p % a.G;
+                    const uint8_t* row = a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2;
+#pragma unroll
+                    for (int i = 0; i < VD; ++i) lds_dma<4>(row, (uint32_t)(64 * i + lane) * 4u, qst + (k * D + 64 * i) * 4);
+                }
             }
+            if (t0 < r_end) {
+                k_unit(t0, 0);
+                v_unit(t0, 0);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");  // Q rows landed
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int j = 0; j < VD; ++j) x[k][j] = ok ? src[lane * VD + j] : 0.0f;
+            for (int k = 0; k < PPW; ++k) {
+                const bool ok = wave + k * NW < npa;
+#pragma unroll
+                for (int j = 0; j < VD; ++j) x[k][j] = ok ? ((const float*)qst)[k * D + lane * VD + j] : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < PPW; ++k) {
+                const int p = wave + k * NW;
+                const bool ok = p < npa;
+                const float* src = (const float*)a.q;
+                if (ok) {
+                    const int qq = p / a.G, h = g_kv * a.G + p % a.G;
+                    src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+                }
+#pragma unroll
+                for (int j = 0; j < VD; ++j) x[k][j] = ok ? src[lane * VD + j] : 0.0f;
+            }
+            if (t0 < r_end) {
+                k_unit(t0, 0);
+                v_unit(t0, 0);
+            }
         }
 #pragma unroll
         for (int k = 0; k < PPW; ++k) {
@@ -377,33 +419,27 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 const int blk = (lane * VD) / kQK;
                 const float dqv = f16_bits_to_f32(f32_to_f16_bits(dblk));
                 ((float*)(img + D))[blk] = dqv;
-                // q4_0: the dot with unsigned nibbles carries +8*sum(q); removed as -8*sum*d_q
-                ((float*)(img + D + 4 * NB))[blk] = KT == XQ_TYPE_Q4_0 ? -8.0f * qs * dqv : 0.0f;
+                // q4_0: the dot with unsigned nibbles carries +8*sum(q); removed as the
+                // exact integer -8*sum(q) before the block scale applies
+                ((int*)(img + D + 4 * NB))[blk] = KT == XQ_TYPE_Q4_0 ? -8 * (int)qs : 0;
             }
         }
-    }
-    __syncthreads();
-
-    // ---- B operands of the score product: pair 16m + lr, elements 8lg..8lg+7 of each block
-    int64_t qb[QUANT ? MT : 1][QUANT ? NB : 1];
-    float dq[QUANT ? MT : 1][QUANT ? NB : 1], qcorr[KT == XQ_TYPE_Q4_0 ? MT : 1][KT == XQ_TYPE_Q4_0 ? NB : 1];
-    h8 qh[QUANT ? 1 : MT][QUANT ? 1 : NB], ql[QUANT ? 1 : MT][QUANT ? 1 : NB];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        const int p = 16 * m + lr;
-        const uint8_t* img = sQ + p * QRB;
-        const float* src = nullptr;  // f32 Q row of the pair (float K)
-        if (!QUANT && p < npa) {
-            const int qq = p / a.G, h = g_kv * a.G + p % a.G;
-            src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+        if (t0 + step < r_end) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // staged Q rows read
+            k_unit(t0 + step, 1);
+            v_unit(t0 + step, 1);
         }
+    } else {
 #pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            if constexpr (QUANT) {
-                qb[m][c] = *(const int64_t*)(img + 32 * c + 8 * lg);
-                dq[m][c] = ((const float*)(img + D))[c];
-                if constexpr (KT == XQ_TYPE_Q4_0) qcorr[m][c] = ((const float*)(img + D + 4 * NB))[c];
-            } else {
+        for (int m = 0; m < MT; ++m) {
+            const int p = 16 * m + lr;
+            const float* src = nullptr;  // f32 Q row of the pair
+            if (p < npa) {
+                const int qq = p / a.G, h = g_kv * a.G + p % a.G;
+                src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+            }
+#pragma unroll
+            for (int c = 0; c < NB; ++c) {
                 // Q = f16 hi + f16 lo (lo = 0 for the NATIVE policy); NaN as ggml's f16 conversion
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
@@ -413,6 +449,34 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     ql[m][c][j] = HI_ONLY ? (_Float16)0.0f
                                             : __builtin_bit_cast(_Float16, (uint16_t)f32_to_f16_bits(xv - f16_bits_to_f32(hb)));
                 }
+            }
+        }
+        if (t0 < r_end) {
+            k_unit(t0, 0);
+            v_unit(t0, 0);
+        }
+        if (t0 + step < r_end) {
+            k_unit(t0 + step, 1);
+            v_unit(t0 + step, 1);
+        }
+    }
+    __syncthreads();
+
+    // ---- B operands of the score product: pair 16m + lr, elements 8lg..8lg+7 of each block
+    int64_t qb[QUANT ? MT : 1][QUANT ? NB : 1];
+    // dqb[m][q]: d_q of block 4q + lg of the lane's pair (the B operand of the
+    // 4-block scale product); qci: the q4_0 correction -8*sum(q) per block
+    float dqb[QUANT ? MT : 1][QUANT ? NB / 4 : 1];
+    int qci[KT == XQ_TYPE_Q4_0 ? MT : 1][KT == XQ_TYPE_Q4_0 ? NB : 1];
+    if constexpr (QUANT) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const uint8_t* img = sQ + (16 * m + lr) * QRB;
+#pragma unroll
+            for (int c = 0; c < NB; ++c) {
+                qb[m][c] = *(const int64_t*)(img + 32 * c + 8 * lg);
+                if (c % 4 == 0) dqb[m][c / 4] = ((const float*)(img + D))[c + lg];
+                if constexpr (KT == XQ_TYPE_Q4_0) qci[m][c] = ((const int*)(img + D + 4 * NB))[c];
             }
         }
     }
@@ -425,59 +489,47 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
         for (int n = 0; n < 2 * NB; ++n) acc[m][n] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // ---- one 16-row slice from ring stage S (S static: the loop is unrolled by two)
-    auto slice = [&](int t, auto stage_tag) {
-        constexpr int S = decltype(stage_tag)::value;
-        // this slice's group is complete once at most one group (the next slice's,
-        // 2 * NIS + 2 * MT instructions, issued later) is outstanding; loads return in order
-        if (t + step < r_end)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_wave_barrier();
-        const uint8_t* Ks = ring + S * 2 * SLICE;
-        const uint8_t* Vs = Ks + SLICE;
-
-        // -- scores s[m][i]: row t + 4lg + i, pair 16m + lr
-        float s[MT][4];
+    // ---- scores s[m][i] of the slice in ring stage ST: row 4lg + i, pair 16m + lr
+    auto scores = [&](auto st_tag, float (&s)[MT][4]) {
+        constexpr int ST = decltype(st_tag)::value;
+        const uint8_t* Ks = ring + ST * 2 * SLICE;
         if constexpr (QUANT) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[m][i] = 0.0f;
-            // blocks in batches: the batch's operand reads, then its independent
-            // MFMAs, then the block-scale arithmetic of the batch
-            constexpr int CB = MT == 1 ? 4 : 2;
+            // blocks in batches of four: the K operand reads, the 4-block f32 product
+            // dks[m][4j + i] = d_k(row 4lg + i, block c0 + j) * d_q(pair, block c0 + j)
+            // (exact: two f16 significands), the independent integer block dots,
+            // then s += dks * float(block dot) as ggml's vec_dot_q8_0_q8_0 /
+            // vec_dot_q4_0_q8_0 accumulate (d = d_k*d_q, then sum += d * sumi)
 #pragma unroll
-            for (int c0 = 0; c0 < NB; c0 += CB) {
-                int64_t ka[CB];
+            for (int c0 = 0; c0 < NB; c0 += 4) {
+                int64_t ka[4];
 #pragma unroll
-                for (int j = 0; j < CB; ++j) ka[j] = k_block_bytes<KT>(Ks + lr * REC, c0 + j, lg);
-                i4 I[MT][CB];
+                for (int j = 0; j < 4; ++j) ka[j] = k_block_bytes<KT>(Ks + lr * REC, c0 + j, lg);
+                // A operand of the scale product: lane (lr, lg) gives d_k of row lr, block c0 + lg
+                const float dkl = (float)*(const _Float16*)(Ks + lr * REC + BB * (c0 + lg));
+                f16v dks[MT];
 #pragma unroll
-                for (int j = 0; j < CB; ++j)
+                for (int m = 0; m < MT; ++m)
+                    dks[m] = __builtin_amdgcn_mfma_f32_16x16x1f32(dkl, dqb[m][c0 / 4], f16v{}, 0, 0, 0);
+                i4 I[MT][4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int m = 0; m < MT; ++m)
                         I[m][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ka[j], qb[m][c0 + j], i4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-                for (int j = 0; j < CB; ++j) {
-                    const int c = c0 + j;
-                    _Float16 dk[4];  // K scales of rows 4lg + i
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) dk[i] = *(const _Float16*)(Ks + (4 * lg + i) * REC + BB * c);
-#pragma unroll
-                    for (int m = 0; m < MT; ++m) {
+                    for (int m = 0; m < MT; ++m)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            float tv = (float)I[m][j][i];
-                            if constexpr (KT == XQ_TYPE_Q4_0)
-                                tv = fmaf(tv, dq[m][c], qcorr[m][c]);
-                            else
-                                tv = tv * dq[m][c];
-                            s[m][i] = fmaf(tv, (float)dk[i], s[m][i]);
+                            int iv = I[m][j][i];
+                            if constexpr (KT == XQ_TYPE_Q4_0) iv += qci[m][c0 + j];
+                            s[m][i] = fmaf((float)iv, dks[m][4 * j + i], s[m][i]);
                         }
-                    }
-                }
             }
         } else {
             f4 sc[MT];
@@ -505,22 +557,144 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[m][i] = sc[m][i];
         }
+    };
 
-        // -- online softmax (base 2); rows past a pair's limit are -inf
-        float x[MT][4];
-        bool grow = false;
-        float mnew[MT];
+    // ---- values of the slice in ring stage ST, block c:
+    //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x P^T
+    auto values = [&](auto st_tag, int c, const h2 (&P)[MT][2]) {
+        constexpr int ST = decltype(st_tag)::value;
+        const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
+        h4 Bv[MT];
+        if constexpr (QUANT) {
+            uint32_t dvw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
+            const uint32_t sel = ((BB * c) & 2) ? 0x07060302u : 0x05040100u;
+            const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[1], dvw[0], sel));
+            const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[3], dvw[2], sel));
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const h2 u = P[m][0] * d01, w = P[m][1] * d23;
+                Bv[m] = h4{u[0], u[1], w[0], w[1]};
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) Bv[m] = h4{P[m][0][0], P[m][0][1], P[m][1][0], P[m][1][1]};
+        }
+        // V^T operands of tiles t = 0, 1: f16 pairs of rows (0,1), (2,3)
+        uint32_t X[4], A0[2], A1[2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint8_t* vr = Vs + (4 * lg + e) * REC;
+            if constexpr (KT == XQ_TYPE_Q8_0)
+                X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
+            else if constexpr (KT == XQ_TYPE_Q4_0)
+                X[e] = *(const uint8_t*)(vr + 18 * c + 2 + lr);
+            else if constexpr (KT == XQ_TYPE_F16)
+                X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
+            else
+                X[e] = lds_u16(vr + 32 * c + 2 * lr);
+        }
+        if constexpr (KT == XQ_TYPE_Q8_0) {
+            q8_vt_f16(X[0], X[1], X[2], X[3], A0, A1);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t x0 = X[2 * e], x1 = X[2 * e + 1];
+                if constexpr (KT == XQ_TYPE_Q4_0) {
+                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+                    const uint32_t w = x0 | (x1 << 16);
+                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
+                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
+                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
+                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
+                } else if constexpr (KT == XQ_TYPE_F16) {
+                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+                } else {
+                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x040c000cu);
+                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x050c010cu);
+                }
+            }
+        }
+        const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
+        const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
+            acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
+        }
+    };
+
+    // ---- one 16-row slice j from ring stage S (S static: the loop is unrolled by
+    //      two). The K unit of slice j+2 is issued once this slice's K and mask
+    //      reads are done, its V unit once the V reads are done, so three units
+    //      are in flight while a slice computes.
+    // Waves w and w + 4 share a SIMD, whose issue arbiter favours the older
+    // wave: left alone, waves 4..7 finish their rows ~25 % later and then run
+    // without a partner while the workgroup waits for them. Each wave posts its
+    // progress and takes issue priority while it is behind its partner (ties go
+    // to the younger wave).
+    int done = 0;
+    if (lane == 0) sProg[wave] = 0;
+    auto balance = [&]() {
+        if constexpr (NW == 8) {
+            const int other = *(volatile int*)&sProg[wave ^ 4];
+            if (done < other || (done == other && wave >= 4))
+                __builtin_amdgcn_s_setprio(1);
+            else
+                __builtin_amdgcn_s_setprio(0);
+        }
+    };
+    auto slice = [&](int t, auto stage_tag) {
+        constexpr int S = decltype(stage_tag)::value;
+        const bool n1 = t + step < r_end, n2 = t + 2 * step < r_end;  // slices j+1, j+2 exist
+        balance();
+        // K_j and mask_j are complete once only the later units are outstanding:
+        // V_j, then (when slice j+1 exists) K_j+1 + mask_j+1 and V_j+1; loads
+        // complete in order
+        if (n1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * NIS + 2 * MT) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NIS) : "memory");
+        __builtin_amdgcn_wave_barrier();
+        float s[MT][4];
+        scores(stage_tag, s);
+
+        // -- the mask pairs of this slice, then the K unit (and mask) of slice j+2
+        //    into the stage this slice's K and mask used
+        uint32_t mw[MT][2];
         const uint8_t* ms = mring + S * MT * 512 + 4 * lane;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const uint32_t mw[2] = {lds_u32(ms + m * 512), lds_u32(ms + m * 512 + 256)};
+            mw[m][0] = lds_u32(ms + m * 512);
+            mw[m][1] = lds_u32(ms + m * 512 + 256);
+        }
+        if (n2) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // K and mask reads of this stage done
+            k_unit(t + 2 * step, S);
+        }
+
+        // -- online softmax (base 2); rows past a pair's limit are -inf
+        float x[MT][4];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const h2 mh = __builtin_bit_cast(h2, mw[i >> 1]);
+                const h2 mh = __builtin_bit_cast(h2, mw[m][i >> 1]);
                 const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
-                const float xv = fmaf(slope2[m], (float)mh[i & 1], v);
-                x[m][i] = t + 4 * lg + i < lim[m] ? xv : -INFINITY;
+                x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
             }
+        if (t + kSub > r_all) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[m][i] = t + 4 * lg + i < lim[m] ? x[m][i] : -INFINITY;
+        }
+        bool grow = false;
+        float mnew[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
             const float mt = xrow_max(fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3])));
             mnew[m] = mt > m_run[m] + kLazyMax ? mt : m_run[m];
             grow |= mnew[m] != m_run[m];
@@ -546,82 +720,31 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             P[m][0] = h2{(_Float16)p[0], (_Float16)p[1]};
             P[m][1] = h2{(_Float16)p[2], (_Float16)p[3]};
         }
-        // -- values: acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x P^T
+        // -- V_j complete: later units K_j+1 + mask, V_j+1, K_j+2 + mask
+        if (n2)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * NIS + 4 * MT) : "memory");
+        else if (n1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int c = 0; c < NB; ++c) {
-            h4 Bv[MT];
-            if constexpr (QUANT) {
-                uint32_t dvw[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
-                const uint32_t sel = ((BB * c) & 2) ? 0x07060302u : 0x05040100u;
-                const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[1], dvw[0], sel));
-                const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[3], dvw[2], sel));
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const h2 u = P[m][0] * d01, w = P[m][1] * d23;
-                    Bv[m] = h4{u[0], u[1], w[0], w[1]};
-                }
-            } else {
-#pragma unroll
-                for (int m = 0; m < MT; ++m) Bv[m] = h4{P[m][0][0], P[m][0][1], P[m][1][0], P[m][1][1]};
-            }
-            // V^T operands of tiles t = 0, 1: f16 pairs of rows (0,1), (2,3)
-            uint32_t X[4], A0[2], A1[2];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint8_t* vr = Vs + (4 * lg + e) * REC;
-                if constexpr (KT == XQ_TYPE_Q8_0)
-                    X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
-                else if constexpr (KT == XQ_TYPE_Q4_0)
-                    X[e] = *(const uint8_t*)(vr + 18 * c + 2 + lr);
-                else if constexpr (KT == XQ_TYPE_F16)
-                    X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
-                else
-                    X[e] = lds_u16(vr + 32 * c + 2 * lr);
-            }
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t x0 = X[2 * e], x1 = X[2 * e + 1];
-                if constexpr (KT == XQ_TYPE_Q8_0) {
-                    A0[e] = i8x2_f16<0>(x0, x1);
-                    A1[e] = i8x2_f16<1>(x0, x1);
-                } else if constexpr (KT == XQ_TYPE_Q4_0) {
-                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
-                    const uint32_t w = x0 | (x1 << 16);
-                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
-                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
-                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
-                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
-                } else if constexpr (KT == XQ_TYPE_F16) {
-                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-                } else {
-                    A0[e] = __builtin_amdgcn_perm(x1, x0, 0x040c000cu);
-                    A1[e] = __builtin_amdgcn_perm(x1, x0, 0x050c010cu);
-                }
-            }
-            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
-            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
-                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
-            }
-        }
+        for (int c = 0; c < NB; ++c) values(stage_tag, c, P);
 
-        // -- refill this stage with the slice two steps ahead
-        const int tr = t + 2 * step;
-        if (tr < r_end) {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads of this stage done
-            stage(tr, S);
-            load_mask(tr, S);
+        // -- the V unit of slice j+2 into the stage this slice's V used
+        if (n2) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V reads of this stage done
+            v_unit(t + 2 * step, S);
         }
+        ++done;
+        if (NW == 8 && lane == 0) *(volatile int*)&sProg[wave] = done;
     };
     for (; t0 < r_end; t0 += 2 * step) {
         slice(t0, std::integral_constant<int, 0>{});
         if (t0 + step < r_end) slice(t0 + step, std::integral_constant<int, 1>{});
     }
+    __builtin_amdgcn_s_setprio(0);
+    if (NW == 8 && lane == 0) *(volatile int*)&sProg[wave] = 1 << 30;  // done: never behind
 
     // ---- merge the wave states per 16-pair group through LDS (fixed wave order)
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
@@ -667,104 +790,12 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
                 *(f4*)(od + 4 * d4) = (o * a1) * inv;
                 if (d4 == 0 && a.lse) a.lse[row] = lse;
-            } else if (a.fused_merge) {
-                // agent-scope stores: visible to the merging workgroup on any XCD
-                // once acknowledged, with no L2 writeback
-                float* po = a.part_o + (row * a.n_splits + split) * D + 4 * d4;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) __hip_atomic_store(po + j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (d4 == 0) {
-                    float* pm = (float*)(a.part_ml + row * a.n_splits + split);
-                    __hip_atomic_store(pm, Mn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(pm + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
             } else {
                 *(f4*)(a.part_o + (row * a.n_splits + split) * D + 4 * d4) = o;
                 if (d4 == 0) a.part_ml[row * a.n_splits + split] = make_float2(Mn, Ls);
             }
         }
         __syncthreads();
-    }
-    if (a.n_splits == 1 || !a.fused_merge) return;
-
-    // ---- the last workgroup of the group merges every split (ascending split order).
-    //      The partial stores above are acknowledged (vmcnt 0) before the arrival is
-    //      counted; the merging workgroup reads them with agent-scope loads.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t gidx = ((uint32_t)b * a.Hkv + g_kv) * a.n_qtiles + qt;
-        sLast = __builtin_amdgcn_atomic_inc32(&g_fa_arrivals[gidx], (uint32_t)(a.n_splits - 1), __ATOMIC_RELAXED, "agent") ==
-                (uint32_t)(a.n_splits - 1);
-    }
-    __syncthreads();
-    if (!sLast) return;
-    const int S = a.n_splits;
-    int* sbad = (int*)smem;  // [npa]: a participating state or a numerator is non-finite
-    for (int p = tid; p < npa; p += NT) sbad[p] = 0;
-    __syncthreads();
-    // item = (pair, 4 dims); each thread merges its items' splits in ascending order
-    constexpr int MAXIT = (NPP * (D / 4) + NT - 1) / NT;
-#pragma unroll
-    for (int it = 0; it < MAXIT; ++it) {
-        const int e = tid + it * NT;
-        if (e >= npa * (D / 4)) continue;
-        const int p = e / (D / 4), d4 = e % (D / 4);
-        const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
-        const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
-        const float* pml = (const float*)(a.part_ml + row * S);
-        const float* po = a.part_o + row * S * D + 4 * d4;
-        float M = -3.402823466e38f;
-        int bad = 0;
-        for (int s0 = 0; s0 < S; ++s0) {
-            const float mv = __hip_atomic_load(pml + 2 * s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float lv = __hip_atomic_load(pml + 2 * s0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (lv != 0.0f) {
-                if (!isfinite(lv) || lv < 0.0f || !isfinite(mv))
-                    bad = 1;
-                else
-                    M = fmaxf(M, mv);
-            }
-        }
-        float Ls = 0.0f;
-        f4 o = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int s0 = 0; s0 < S; ++s0) {
-            const float mv = __hip_atomic_load(pml + 2 * s0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float lv = __hip_atomic_load(pml + 2 * s0 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            f4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                v[j] = __hip_atomic_load(po + (int64_t)s0 * D + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (lv != 0.0f) {
-                const float w = expf(mv - M);
-                Ls = fmaf(lv, w, Ls);
-                o += v * w;
-            }
-        }
-        int badl = bad || !isfinite(Ls);
-        float a1, inv, lse;
-        fa_finalize(Ls == 0.0f ? -INFINITY : M, Ls, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
-        if (!isfinite(inv) || (Ls != 0.0f && !isfinite(lse))) badl = 1;
-        o = (o * a1) * inv;
-        if (a.poison && (badl || !(isfinite(o[0]) && isfinite(o[1]) && isfinite(o[2]) && isfinite(o[3]))))
-            atomicOr(&sbad[p], 1);
-        float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
-        *(f4*)(od + 4 * d4) = o;
-        if (d4 == 0 && a.lse) a.lse[row] = lse;
-    }
-    if (!a.poison) return;
-    __syncthreads();
-    // poison: any non-finite participating state or numerator makes the whole row NaN
-#pragma unroll
-    for (int it = 0; it < MAXIT; ++it) {
-        const int e = tid + it * NT;
-        if (e >= npa * (D / 4)) continue;
-        const int p = e / (D / 4), d4 = e % (D / 4);
-        if (!sbad[p]) continue;
-        const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
-        float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
-        *(f4*)(od + 4 * d4) = f4{NAN, NAN, NAN, NAN};
-        if (d4 == 0 && a.lse) a.lse[(int64_t)b * rows_per_seq + (int64_t)iq * a.H + h] = NAN;
     }
 }
 
@@ -838,10 +869,6 @@ bool fa_mma_mask_ok(const FaArgs& a) {
     return !a.mask || ((uintptr_t)a.mask % 4 == 0 && a.m_nb1 % 4 == 0 && a.m_nb2 % 4 == 0 && a.m_nb3 % 4 == 0);
 }
 
-bool fa_mma_fused_merge(int64_t n_groups, int n_pairs, int n_splits) {
-    return n_splits > 1 && n_groups <= kMaxGroups && (int64_t)n_pairs * n_splits <= kFusedMergeMax;
-}
-
 hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
     const int D = (int)L.q->ne[0];
     const int kt = L.k->type;
@@ -855,8 +882,6 @@ hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
     a.q_nb1 = (int64_t)L.q->nb[1];
     a.q_nb2 = (int64_t)L.q->nb[2];
     a.q_nb3 = (int64_t)L.q->nb[3];
-    const int64_t n_groups = (int64_t)a.B * a.Hkv * a.n_qtiles;
-    a.fused_merge = fa_mma_fused_merge(n_groups, a.QT * a.G, a.n_splits) ? 1 : 0;
     if (!fa_mma_mask_ok(a)) return hipErrorInvalidValue;
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     {
@@ -864,7 +889,7 @@ hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
         hipLaunchKernelGGL(fn, dim3(n_wg), dim3(64 * waves), 0, stream, a);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.n_splits == 1 || a.fused_merge) return e;
+    if (e != hipSuccess || a.n_splits == 1) return e;
     return fa_reduce_launch(a, D, stream);
 }
 
