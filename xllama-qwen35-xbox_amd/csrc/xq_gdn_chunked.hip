@@ -3,52 +3,55 @@
 // The recurrence of shaders/ggml_d3d12_gated_delta_net.hlsl:40-85, per v-head
 // and value column c (state column s in R^128, k-head = v-head % 16):
 //   s *= e^{g_t};  u_t = beta_t (v_t[c] - s . k_t);  s += k_t u_t;  y_t[c] = scale * s . q_t
-// is computed 64 tokens at a time in the WY / UT form of the delta rule.
-// With G_t = g_1 + ... + g_t inside the chunk (cumulative log-decay) and S_0
-// the state entering the chunk (S[i][c], key dim i, value column c):
+// is computed 64 tokens at a time in the UT form of the delta rule. With
+// G_t = g_1 + ... + g_t inside the chunk (cumulative log-decay), S the state
+// entering the chunk (S[i][c], key dim i, value column c), K, Q, V the chunk's
+// rows and
 //   L[t][j] = beta_t e^{G_t - G_j} (k_t . k_j)  (j < t),   T = (I + L)^{-1} diag(beta)
-//   U = W_v - W_k S_0,  W_v = T V,  W_k = T diag(e^G) K
-//   Y = scale (diag(e^G) Q S_0 + P U),  P[t][j] = (q_t . k_j) e^{G_t - G_j}  (j <= t)
-//   S_C = e^{G_C} S_0 + K^T diag(e^{G_C - G}) U
+//   P[t][j] = (q_t . k_j) e^{G_t - G_j}  (j <= t)
+// the chunk is
+//   U  = T (V - diag(e^G) K S)
+//   Y  = scale (diag(e^G) Q S + P U)
+//   S' = e^{G_C} S + K^T diag(e^{G_C - G}) U
 // which equals the token-by-token recurrence in exact arithmetic.
 //
 // Two kernels:
 //   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
-//                   parallel: K K^T and Q K^T on f16 MFMA (products of the
-//                   f16-converted bf16/f32 inputs, f32 accumulation), the unit
-//                   lower-triangular solve for T in f32, W_k, W_v on f16 MFMA
-//                   with T split into f16 hi + lo parts, P with its decays;
-//                   stores W_k, W_v, P (f16 hi + lo planes), Q and K^T (f16) and
-//                   the decay vectors in the workspace;
-//   gdn_chunk_scan  one workgroup per (sequence, v-head, 32-column block) runs
-//                   the chunks in order with its 128 x 32 state block in
-//                   registers (f32): U, Y and the next state on f16 MFMA, f32
-//                   operands split into hi + lo (about 22 significant bits), so
-//                   the result stays within f32-recurrence tolerances.
-// MFMA operand layouts (v_mfma_f32_16x16x16_f16): A lane (m = l % 16,
-// k = 4 (l / 16) .. +3), B lane (n = l % 16, same k), C lane (rows
-// 4 (l / 16) + r, column l % 16). An output tile whose rows are the next
-// product's contraction index is that product's B operand as it stands.
+//                   parallel: K K^T and Q K^T on f16 MFMA (f32 accumulation),
+//                   the unit lower-triangular solve for T in f32, P with its
+//                   decays; stores T and P as f16 hi + lo planes, K^T as f16
+//                   and the decay vectors (49 KB per chunk) in the workspace.
+//   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
+//                   the chunks in order with its 128 x 16 state block in
+//                   registers (f32). Every MFMA operand that does not depend on
+//                   the state (K and Q rows straight from the inputs, as f16:
+//                   exact for bf16 rows; K^T, T and P rows from the workspace;
+//                   V and the decays) is loaded into registers a chunk ahead;
+//                   LDS carries only the state-dependent exchanges (S^T, X^T,
+//                   U^T). The products run on v_mfma_f32_16x16x32_f16 with f32
+//                   operands split into f16 hi + lo (about 22 significant bits),
+//                   so the result stays within f32-recurrence tolerances.
+// The 8 column blocks of a head run on one XCD (consecutive logical workgroups)
+// so the chunk rows and T, P they share are read from HBM once.
 #include "xq_kernels.h"
 
 namespace xq {
 
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;
-constexpr int kCols = 32;  // value columns per scan workgroup
+constexpr int kCols = 16;            // value columns per scan workgroup
+constexpr int kColBlocks = 128 / kCols;
 
 // Workspace record of one (sequence, v-head, chunk), byte offsets.
-constexpr int kRecWkHi = 0;                      // f16 [64][128]
-constexpr int kRecWkLo = kRecWkHi + 64 * 128 * 2;
-constexpr int kRecWvHi = kRecWkLo + 64 * 128 * 2;  // f16 [64][128]
-constexpr int kRecWvLo = kRecWvHi + 64 * 128 * 2;
-constexpr int kRecPHi = kRecWvLo + 64 * 128 * 2;   // f16 [64][64]
+constexpr int kRecTHi = 0;                       // f16 [64][64]
+constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
+constexpr int kRecPHi = kRecTLo + 64 * 64 * 2;  // f16 [64][64]
 constexpr int kRecPLo = kRecPHi + 64 * 64 * 2;
-constexpr int kRecQ = kRecPLo + 64 * 64 * 2;       // f16 [64][128]
-constexpr int kRecKT = kRecQ + 64 * 128 * 2;       // f16 [128][64]
-constexpr int kRecDec = kRecKT + 128 * 64 * 2;     // f32 eG[64], eGCG[64], eGC
+constexpr int kRecKT = kRecPLo + 64 * 64 * 2;  // f16 K^T [128][64]
+constexpr int kRecDec = kRecKT + 128 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}
 constexpr int kRecBytes = kRecDec + 1024;
 
 struct GdnChunkArgs {
@@ -67,8 +70,9 @@ struct GdnChunkArgs {
     int64_t g_nb1, g_nb2, g_nb3;
     int64_t b_nb1, b_nb2, b_nb3;
     int64_t s_nb3, dst_nb2, so_nb3;
-    int32_t T;  // tokens processed here (multiple chunks, last one partial)
+    int32_t T;  // tokens processed here (several chunks, the last one partial)
     int32_t n_chunks;
+    int32_t B;
     float scale;
 };
 
@@ -76,29 +80,54 @@ struct GdnChunkArgs {
 XQ_DEV _Float16 f16_hi(float x) { return (_Float16)x; }
 XQ_DEV _Float16 f16_lo(float x) { return (_Float16)(x - (float)(_Float16)x); }
 
-template <bool BF16>
-XQ_DEV float in_elem(const uint8_t* row, int i) {
-    if constexpr (BF16)
-        return bf16_bits_to_f32(((const uint16_t*)row)[i]);
-    else
-        return ((const float*)row)[i];
+// Eight consecutive elements of an input row (bf16 or f32) as f32; VEC reads
+// them with 16-byte loads (the host checks the alignment).
+template <bool BF16, bool VEC>
+XQ_DEV void load8(const uint8_t* row, int i0, float (&x)[8]) {
+    if constexpr (VEC && BF16) {
+        const uint4 w = *(const uint4*)(row + 2 * i0);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = bf16_bits_to_f32(u[e] & 0xffffu);
+            x[2 * e + 1] = bf16_bits_to_f32(u[e] >> 16);
+        }
+    } else if constexpr (VEC) {
+        const float4 a = *(const float4*)(row + 4 * i0);
+        const float4 b = *(const float4*)(row + 4 * i0 + 16);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            x[e] = BF16 ? bf16_bits_to_f32(((const uint16_t*)row)[i0 + e]) : ((const float*)row)[i0 + e];
+    }
 }
+
+XQ_DEV h8 to_h8(const float (&x)[8]) {
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)x[e];
+    return r;
+}
+
+XQ_DEV f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
 // ---------------------------------------------------------------- prep
 
-template <bool BF16>
-__global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
-    constexpr int KP = 136;  // padded f16 row strides
-    constexpr int TP = 72;
+template <bool BF16, bool VEC>
+__global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
+    constexpr int KP = 136;  // padded f16 row stride (halves)
+    constexpr int TP = 72;   // K^T row stride (halves)
     constexpr int FP = 65;   // padded f32 row stride
-    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i]
+    // 68.6 KB: two workgroups per CU. sKT holds K^T for the record; after the
+    // products sK becomes T and sQ the P planes.
+    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][65]
     __shared__ __attribute__((aligned(16))) _Float16 sKT[128 * TP];  // K^T [i][t]
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[64 * KP];    // Q [t][i]
-    __shared__ __attribute__((aligned(16))) _Float16 sVT[128 * TP];  // V^T [c][t]
+    __shared__ __attribute__((aligned(16))) _Float16 sQ[64 * KP];    // Q [t][i], then P hi, lo [64][64]
     __shared__ float sKK[64 * FP];  // K K^T, then L
-    __shared__ float sQK[64 * FP];  // Q K^T
-    __shared__ float sT[64 * FP];   // T [t][j]
     __shared__ float sG[64], sBeta[64], sEG[64];
+    static_assert(64 * FP * 4 <= 64 * KP * 2 && 2 * 64 * 64 * 2 <= 64 * KP * 2, "LDS aliases");
 
     const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int kh = h % 16;
@@ -106,24 +135,30 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
     const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
     const int t0 = n * kChunk;
 
-    // ---- chunk rows -> LDS as f16 (tokens past T are zero, with g = beta = 0)
+    // ---- chunk rows -> LDS as f16 (tokens past T are zero, with g = beta = 0):
+    //      thread = (token, quarter of 32 elements), 8 elements per load
     {
-        const int t = tid >> 2, qtr = tid & 3;  // 64 tokens x 4 quarters of 32 elements
+        const int t = tid >> 2, qt = tid & 3;
         const int tg = t0 + t;
         const bool ok = tg < a.T;
         const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tg * a.k_nb2 + (int64_t)kh * a.k_nb1;
         const uint8_t* qr = a.q + (int64_t)b * a.q_nb3 + (int64_t)tg * a.q_nb2 + (int64_t)kh * a.q_nb1;
-        const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tg * a.v_nb2 + (int64_t)h * a.v_nb1;
-#pragma unroll 8
-        for (int e = 0; e < 32; ++e) {
-            const int i = qtr * 32 + e;
-            const _Float16 kv = ok ? (_Float16)in_elem<BF16>(kr, i) : (_Float16)0.0f;
-            const _Float16 qv = ok ? (_Float16)in_elem<BF16>(qr, i) : (_Float16)0.0f;
-            const _Float16 vv = ok ? (_Float16)in_elem<BF16>(vr, i) : (_Float16)0.0f;
-            sK[t * KP + i] = kv;
-            sKT[i * TP + t] = kv;
-            sQ[t * KP + i] = qv;
-            sVT[i * TP + t] = vv;
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) {
+            const int i0 = 32 * qt + 8 * gi;
+            float xk[8], xq[8];
+            if (ok) {
+                load8<BF16, VEC>(kr, i0, xk);
+                load8<BF16, VEC>(qr, i0, xq);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xk[e] = xq[e] = 0.0f;
+            }
+            const h8 hk = to_h8(xk);
+            *(h8*)(sK + t * KP + i0) = hk;
+            *(h8*)(sQ + t * KP + i0) = to_h8(xq);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sKT[(i0 + e) * TP + t] = hk[e];
         }
         if (tid < 64) {
             const int tt = t0 + tid;
@@ -137,31 +172,44 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
     if (tid < 64) {
         float G = 0.0f;
         for (int s = 0; s <= tid; ++s) G += sG[s];
-        sEG[tid] = G;  // G for now, exponentiated below
+        sEG[tid] = G;
     }
     // ---- K K^T and Q K^T: 16 tiles each, 4 per wave, contraction over 128 key dims
+    f4 qk[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
         const int tile = wave * 4 + tt;
         const int mt = tile >> 2, nt = tile & 3;
-        f4 kk = f4{0.0f, 0.0f, 0.0f, 0.0f}, qk = kk;
+        f4 kk = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        qk[tt] = kk;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const h4 bk = *(const h4*)(sK + (nt * 16 + lr) * KP + ks * 16 + 4 * lg);
-            const h4 ak = *(const h4*)(sK + (mt * 16 + lr) * KP + ks * 16 + 4 * lg);
-            const h4 aq = *(const h4*)(sQ + (mt * 16 + lr) * KP + ks * 16 + 4 * lg);
-            kk = __builtin_amdgcn_mfma_f32_16x16x16f16(ak, bk, kk, 0, 0, 0);
-            qk = __builtin_amdgcn_mfma_f32_16x16x16f16(aq, bk, qk, 0, 0, 0);
+        for (int ks = 0; ks < 4; ++ks) {
+            const h8 bk = *(const h8*)(sK + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
+            const h8 ak = *(const h8*)(sK + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
+            const h8 aq = *(const h8*)(sQ + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
+            kk = mfma32(ak, bk, kk);
+            qk[tt] = mfma32(aq, bk, qk[tt]);
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sKK[(mt * 16 + 4 * lg + r) * FP + nt * 16 + lr] = kk[r];
+    }
+    __syncthreads();  // K, Q no longer read; G ready
+    // ---- P = (Q K^T) e^{G_t - G_j} (j <= t) as f16 hi, lo planes in place of Q
+    _Float16* sPh = sQ;
+    _Float16* sPl = sQ + 64 * 64;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        const int tile = wave * 4 + tt;
+        const int mt = tile >> 2, nt = tile & 3;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = mt * 16 + 4 * lg + r, col = nt * 16 + lr;
-            sKK[row * FP + col] = kk[r];
-            sQK[row * FP + col] = qk[r];
+            const int t = mt * 16 + 4 * lg + r, j = nt * 16 + lr;
+            const float pv = j <= t ? qk[tt][r] * __expf(sEG[t] - sEG[j]) : 0.0f;
+            sPh[t * 64 + j] = f16_hi(pv);
+            sPl[t * 64 + j] = f16_lo(pv);
         }
     }
-    __syncthreads();
-    // ---- L (strictly lower, in place of K K^T); decays e^{G}
+    // ---- L (strictly lower, in place of K K^T)
     for (int e = tid; e < 64 * 64; e += 256) {
         const int t = e >> 6, j = e & 63;
         const float L = j < t ? sBeta[t] * __expf(sEG[t] - sEG[j]) * sKK[t * FP + j] : 0.0f;
@@ -170,6 +218,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
     __syncthreads();
     // ---- T = (I + L)^{-1} diag(beta): column j by a quad of lanes; lane part p
     //      keeps x_s for s in [16p, 16p + 16) and the quad sums the dot products
+    //      (four partial chains per lane)
+    float* sT = (float*)sK;  // T [t][j], f32
     {
         const int j = wave * 16 + (lane >> 2), p = lane & 3;
         float x[16];
@@ -181,8 +231,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
             float part = 0.0f;
             if (t > 0) {
                 const float* Lr = sKK + t * FP + 16 * p;
+                float c4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int m = 0; m < 16; ++m) part = fmaf(Lr[m], x[m], part);  // L[t][s >= t] = 0
+                for (int m = 0; m < 16; ++m) c4[m & 3] = fmaf(Lr[m], x[m], c4[m & 3]);  // L[t][s >= t] = 0
+                part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
             }
             part += dpp<0xB1>(part);  // quad: lanes p ^ 1
             part += dpp<0x4E>(part);  // quad: lanes p ^ 2
@@ -192,201 +244,284 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnChunkArgs a) {
 #pragma unroll
         for (int m = 0; m < 16; ++m) sT[(16 * p + m) * FP + j] = x[m];
     }
+    __syncthreads();
+
+    // ---- the record: T (f16 hi + lo), P (hi, lo), K^T (f16) with 16-byte
+    //      stores, and the decays
+    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+    {
+        const int t = tid >> 2, j0 = 16 * (tid & 3);
+        h8 th[2], tl[2];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float tv = sT[t * FP + j0 + e];
+            th[e >> 3][e & 7] = f16_hi(tv), tl[e >> 3][e & 7] = f16_lo(tv);
+        }
+        const int o = (t * 64 + j0) * 2;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            *(h8*)(rec + kRecTHi + o + 16 * u) = th[u];
+            *(h8*)(rec + kRecTLo + o + 16 * u) = tl[u];
+            *(h8*)(rec + kRecPHi + o + 16 * u) = *(const h8*)(sPh + t * 64 + j0 + 8 * u);
+            *(h8*)(rec + kRecPLo + o + 16 * u) = *(const h8*)(sPl + t * 64 + j0 + 8 * u);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {  // K^T: 1024 chunks of 8 tokens
+        const int e = tid + 256 * u, i = e >> 3, c8 = e & 7;
+        *(h8*)(rec + kRecKT + (i * 64 + 8 * c8) * 2) = *(const h8*)(sKT + i * TP + 8 * c8);
+    }
     if (tid < 64) {
         const float GC = sEG[63];
         const float G = sEG[tid];
-        float* dec = (float*)(a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes + kRecDec);
+        float* dec = (float*)(rec + kRecDec);
         dec[tid] = __expf(G);
         dec[64 + tid] = __expf(GC - G);
         if (tid == 0) dec[128] = __expf(GC);
-    }
-    __syncthreads();
-
-    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
-    // ---- W_k = T diag(e^G) K and W_v = T V: 32 tiles each (64 x 128), 8 per wave
-#pragma unroll 2
-    for (int tt = 0; tt < 8; ++tt) {
-        const int tile = wave * 8 + tt;
-        const int mt = tile >> 3, nt = tile & 7;
-        f4 wk = f4{0.0f, 0.0f, 0.0f, 0.0f}, wv = wk;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            const int j0 = ks * 16 + 4 * lg;
-            h4 th, tl, tph, tpl;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float tv = sT[(mt * 16 + lr) * FP + j0 + e];
-                th[e] = f16_hi(tv), tl[e] = f16_lo(tv);
-                tph[e] = f16_hi(tv * __expf(sEG[j0 + e])), tpl[e] = f16_lo(tv * __expf(sEG[j0 + e]));
-            }
-            const h4 bk = *(const h4*)(sKT + (nt * 16 + lr) * TP + j0);
-            const h4 bv = *(const h4*)(sVT + (nt * 16 + lr) * TP + j0);
-            wk = __builtin_amdgcn_mfma_f32_16x16x16f16(tph, bk, wk, 0, 0, 0);
-            wk = __builtin_amdgcn_mfma_f32_16x16x16f16(tpl, bk, wk, 0, 0, 0);
-            wv = __builtin_amdgcn_mfma_f32_16x16x16f16(th, bv, wv, 0, 0, 0);
-            wv = __builtin_amdgcn_mfma_f32_16x16x16f16(tl, bv, wv, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = mt * 16 + 4 * lg + r, col = nt * 16 + lr;
-            _Float16 hi, lo;
-            hi = f16_hi(wk[r]), lo = f16_lo(wk[r]);
-            ((_Float16*)(rec + kRecWkHi))[row * 128 + col] = hi;
-            ((_Float16*)(rec + kRecWkLo))[row * 128 + col] = lo;
-            hi = f16_hi(wv[r]), lo = f16_lo(wv[r]);
-            ((_Float16*)(rec + kRecWvHi))[row * 128 + col] = hi;
-            ((_Float16*)(rec + kRecWvLo))[row * 128 + col] = lo;
-        }
-    }
-    // ---- P (with the diagonal), Q and K^T copies
-    for (int e = tid; e < 64 * 64; e += 256) {
-        const int t = e >> 6, j = e & 63;
-        const float pv = j <= t ? sQK[t * FP + j] * __expf(sEG[t] - sEG[j]) : 0.0f;
-        _Float16 hi, lo;
-        hi = f16_hi(pv), lo = f16_lo(pv);
-        ((_Float16*)(rec + kRecPHi))[e] = hi;
-        ((_Float16*)(rec + kRecPLo))[e] = lo;
-    }
-    for (int e = tid; e < 64 * 128; e += 256) {
-        const int t = e >> 7, i = e & 127;
-        ((_Float16*)(rec + kRecQ))[e] = sQ[t * KP + i];
-        const int ii = e >> 6, tt = e & 63;
-        ((_Float16*)(rec + kRecKT))[e] = sKT[ii * TP + tt];
     }
 }
 
 // ---------------------------------------------------------------- scan
 
-__global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
-    constexpr int SP = 136;  // S^T row stride (halves): [c][i]
-    constexpr int UP = 72;   // U^T row stride: [c][t]
-    __shared__ __attribute__((aligned(16))) _Float16 sSh[kCols * SP], sSl[kCols * SP];
-    __shared__ __attribute__((aligned(16))) _Float16 sUh[kCols * UP], sUl[kCols * UP];
-    __shared__ __attribute__((aligned(16))) _Float16 sVh[kCols * UP], sVl[kCols * UP];  // U' = e^{G_C - G} U
+// Operands of one chunk for one wave of a scan workgroup, loaded a chunk ahead:
+// A operands (row 16w + lr of the wave's token tile, k = 32 ks + 8 lg .. +7) of
+// K and Q (raw input words, decoded when used), of T and P (hi, lo), and of
+// K^T for the wave's key-dim tiles 2w, 2w + 1; the raw V values and e^G,
+// e^{G_C - G} of the lane's four tokens 16w + 4lg + r (column 16cb + lr), and
+// e^{G_C}. Every load is unconditional (token and chunk indices are clamped
+// into range and out-of-range tokens masked at use), so the compiler's waits
+// for a chunk's operands never include the next chunk's loads.
+template <bool BF16, bool VEC>
+struct ScanOps {
+    static constexpr int KW = VEC ? (BF16 ? 1 : 2) : 4;  // 16-byte words per 8 elements (VEC), else raw dwords
+    uint4 kw[4][KW], qw[4][KW];
+    h8 th[2], tl[2], ph[2], pl[2], kt[2][2];
+    uint32_t vw[4];
+    float4 eg, egc;
+    float eGC;
+    bool ok;        // the A-operand token is in range
+    uint32_t vok;   // bit r: token 16w + 4lg + r is in range
+};
 
-    const int cb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
-    const float* st = a.state + (int64_t)b * (a.s_nb3 / 4) + (int64_t)h * 16384;
+// 8 elements of a K / Q row: raw words at element i0
+template <bool BF16, bool VEC, int KW>
+XQ_DEV void load_raw8(const uint8_t* row, int i0, uint4 (&w)[KW]) {
+    if constexpr (VEC) {
+        const uint8_t* p = row + (BF16 ? 2 : 4) * i0;
+#pragma unroll
+        for (int u = 0; u < KW; ++u) w[u] = *(const uint4*)(p + 16 * u);
+    } else {
+        uint32_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            e[j] = BF16 ? (uint32_t)((const uint16_t*)row)[i0 + j] : ((const uint32_t*)row)[i0 + j];
+        w[0] = make_uint4(e[0], e[1], e[2], e[3]);
+        w[1] = make_uint4(e[4], e[5], e[6], e[7]);
+        w[2] = w[3] = make_uint4(0, 0, 0, 0);
+    }
+}
 
-    // state tiles owned by this wave: key-dim tiles 2w, 2w + 1, column tiles 0, 1;
-    // lane holds S[i = 16 it + 4 lg + r][c = 32 cb + 16 ct + lr]
-    f4 S[2][2];
+template <bool BF16, bool VEC, int KW>
+XQ_DEV h8 decode8(const uint4 (&w)[KW], bool ok) {
+    float x[8];
+    if constexpr (VEC && BF16) {
+        const uint32_t u[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
 #pragma unroll
-    for (int a2 = 0; a2 < 2; ++a2)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int it = 2 * wave + a2;
-            const int c = kCols * cb + 16 * ct + lr;
-            const float4 v = *(const float4*)(st + (int64_t)c * 128 + 16 * it + 4 * lg);
-            S[a2][ct] = f4{v.x, v.y, v.z, v.w};
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = bf16_bits_to_f32(u[e] & 0xffffu);
+            x[2 * e + 1] = bf16_bits_to_f32(u[e] >> 16);
         }
-    float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
+    } else {
+        const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = BF16 ? bf16_bits_to_f32(u[e] & 0xffffu) : __uint_as_float(u[e]);
+    }
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = ok ? (_Float16)x[e] : (_Float16)0.0f;
+    return r;
+}
 
-    for (int n = 0; n < a.n_chunks; ++n) {
-        const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
-        const _Float16* Wkh = (const _Float16*)(rec + kRecWkHi);
-        const _Float16* Wkl = (const _Float16*)(rec + kRecWkLo);
-        const _Float16* Wvh = (const _Float16*)(rec + kRecWvHi);
-        const _Float16* Wvl = (const _Float16*)(rec + kRecWvLo);
-        const _Float16* Ph = (const _Float16*)(rec + kRecPHi);
-        const _Float16* Pl = (const _Float16*)(rec + kRecPLo);
-        const _Float16* Qh = (const _Float16*)(rec + kRecQ);
-        const _Float16* KT = (const _Float16*)(rec + kRecKT);
-        const float* dec = (const float*)(rec + kRecDec);
-
-        // ---- S (hi, lo) -> LDS as S^T [c][i]: B operand rows
+template <bool BF16, bool VEC>
+XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wave, int lr, int lg,
+                      ScanOps<BF16, VEC>& L) {
+    const int kh = h % 16;
+    n = min(n, a.n_chunks - 1);  // the prefetch past the last chunk re-reads it
+    {
+        const int tg = n * kChunk + 16 * wave + lr;  // A-operand row token
+        L.ok = tg < a.T;
+        const int tc = min(tg, a.T - 1);
+        const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tc * a.k_nb2 + (int64_t)kh * a.k_nb1;
+        const uint8_t* qr = a.q + (int64_t)b * a.q_nb3 + (int64_t)tc * a.q_nb2 + (int64_t)kh * a.q_nb1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            load_raw8<BF16, VEC>(kr, 32 * ks + 8 * lg, L.kw[ks]);
+            load_raw8<BF16, VEC>(qr, 32 * ks + 8 * lg, L.qw[ks]);
+        }
+    }
+    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int o = ((16 * wave + lr) * 64 + 32 * ks + 8 * lg) * 2;
+        L.th[ks] = *(const h8*)(rec + kRecTHi + o);
+        L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
+        L.ph[ks] = *(const h8*)(rec + kRecPHi + o);
+        L.pl[ks] = *(const h8*)(rec + kRecPLo + o);
 #pragma unroll
         for (int a2 = 0; a2 < 2; ++a2)
+            L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2);
+    }
+    const float* dec = (const float*)(rec + kRecDec);
+    L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
+    L.egc = *(const float4*)(dec + 64 + 16 * wave + 4 * lg);
+    L.eGC = dec[128];
+    L.vok = 0;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
+    for (int r = 0; r < 4; ++r) {
+        const int tg = n * kChunk + 16 * wave + 4 * lg + r;
+        L.vok |= (tg < a.T ? 1u : 0u) << r;
+        const int tc = min(tg, a.T - 1);
+        const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tc * a.v_nb2 + (int64_t)h * a.v_nb1;
+        const int c = kCols * cb + lr;
+        L.vw[r] = BF16 ? (uint32_t)((const uint16_t*)vr)[c] : ((const uint32_t*)vr)[c];
+    }
+}
+
+template <bool BF16, bool VEC>
+__global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
+    constexpr int TP = 72;   // X^T, U^T rows [c][t] (halves)
+    constexpr int SP = 136;  // S^T rows [c][i] (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 sSh[kCols * SP], sSl[kCols * SP];  // S^T hi, lo
+    __shared__ __attribute__((aligned(16))) _Float16 sXh[kCols * TP], sXl[kCols * TP];  // X^T
+    __shared__ __attribute__((aligned(16))) _Float16 sUh[kCols * TP], sUl[kCols * TP];  // U^T
+    __shared__ __attribute__((aligned(16))) _Float16 sWh[kCols * TP], sWl[kCols * TP];  // (e^{G_C - G} U)^T
+
+    const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
+    const uint32_t wg = xcd_remap(blockIdx.x, n_wg);  // column blocks of a head adjacent (one XCD)
+    const int cb = (int)(wg % kColBlocks);
+    const int h = (int)((wg / kColBlocks) % 32);
+    const int b = (int)(wg / (kColBlocks * 32));
+    const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
+
+    // state tiles of this wave: key-dim tiles 2w, 2w + 1 of the 128 x 16 block;
+    // lane holds S[i = 16 it + 4 lg + r][c = 16 cb + lr]
+    const float* st = a.state + (int64_t)b * (a.s_nb3 / 4) + (int64_t)h * 16384;
+    f4 S[2];
+#pragma unroll
+    for (int a2 = 0; a2 < 2; ++a2) {
+        const int it = 2 * wave + a2;
+        const float4 v = *(const float4*)(st + (int64_t)(kCols * cb + lr) * 128 + 16 * it + 4 * lg);
+        S[a2] = f4{v.x, v.y, v.z, v.w};
+    }
+    float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
+
+    ScanOps<BF16, VEC> ops[2];
+    scan_load<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
+    for (int n = 0; n < a.n_chunks; n += 2) {
+        // two chunks per iteration so the operand sets stay in fixed registers
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            const int nn = n + par;
+            if (nn >= a.n_chunks) break;
+            ScanOps<BF16, VEC>& C = ops[par];
+            scan_load<BF16, VEC>(a, b, h, cb, nn + 1, wave, lr, lg, ops[par ^ 1]);
+
+            // ---- S (hi, lo) -> LDS as S^T [c][i]: the B operand rows of K S and Q S
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2) {
                 const int it = 2 * wave + a2;
-                h4 hi, lo;
+                h4 sh, sl;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) hi[r] = f16_hi(S[a2][ct][r]), lo[r] = f16_lo(S[a2][ct][r]);
-                *(h4*)(sSh + (16 * ct + lr) * SP + 16 * it + 4 * lg) = hi;
-                *(h4*)(sSl + (16 * ct + lr) * SP + 16 * it + 4 * lg) = lo;
+                for (int r = 0; r < 4; ++r) sh[r] = f16_hi(S[a2][r]), sl[r] = f16_lo(S[a2][r]);
+                *(h4*)(sSh + lr * SP + 16 * it + 4 * lg) = sh;
+                *(h4*)(sSl + lr * SP + 16 * it + 4 * lg) = sl;
             }
-        __syncthreads();
+            __syncthreads();
 
-        // ---- U = W_v - W_k S and Q S for token tile w (16 tokens), both column tiles
-        f4 U[2], QS[2];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, accq = acc;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const int arow = (16 * wave + lr) * 128 + 16 * ks + 4 * lg;
-                const h4 ah = *(const h4*)(Wkh + arow), al = *(const h4*)(Wkl + arow), aq = *(const h4*)(Qh + arow);
-                const h4 bh = *(const h4*)(sSh + (16 * ct + lr) * SP + 16 * ks + 4 * lg);
-                const h4 bl = *(const h4*)(sSl + (16 * ct + lr) * SP + 16 * ks + 4 * lg);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
-                accq = __builtin_amdgcn_mfma_f32_16x16x16f16(aq, bh, accq, 0, 0, 0);
-                accq = __builtin_amdgcn_mfma_f32_16x16x16f16(aq, bl, accq, 0, 0, 0);
-            }
-            QS[ct] = accq;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * wave + 4 * lg + r, c = kCols * cb + 16 * ct + lr;
-                U[ct][r] = ((float)Wvh[t * 128 + c] + (float)Wvl[t * 128 + c]) - acc[r];
-            }
-            // U and U' = e^{G_C - G_t} U (hi, lo) -> LDS as U^T [c][t]
-            h4 uh, ul, vh, vl;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * wave + 4 * lg + r;
-                uh[r] = f16_hi(U[ct][r]), ul[r] = f16_lo(U[ct][r]);
-                vh[r] = f16_hi(U[ct][r] * dec[64 + t]), vl[r] = f16_lo(U[ct][r] * dec[64 + t]);
-            }
-            const int o = (16 * ct + lr) * UP + 16 * wave + 4 * lg;
-            *(h4*)(sUh + o) = uh;
-            *(h4*)(sUl + o) = ul;
-            *(h4*)(sVh + o) = vh;
-            *(h4*)(sVl + o) = vl;
-        }
-        __syncthreads();
-
-        // ---- Y = scale (diag(e^G) Q S + P U) for token tile w
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            f4 acc;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = QS[ct][r] * dec[16 * wave + 4 * lg + r];
+            // ---- K S and Q S for token tile w (16 tokens x 16 columns)
+            f4 ksh = f4{0.0f, 0.0f, 0.0f, 0.0f}, ksl = ksh, qsh = ksh, qsl = ksh;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const int arow = (16 * wave + lr) * 64 + 16 * ks + 4 * lg;
-                const h4 ah = *(const h4*)(Ph + arow), al = *(const h4*)(Pl + arow);
-                const int bo = (16 * ct + lr) * UP + 16 * ks + 4 * lg;
-                const h4 bh = *(const h4*)(sUh + bo), bl = *(const h4*)(sUl + bo);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
+                const h8 ak = decode8<BF16, VEC>(C.kw[ks], C.ok), aq = decode8<BF16, VEC>(C.qw[ks], C.ok);
+                const int bo = lr * SP + 32 * ks + 8 * lg;
+                const h8 bh = *(const h8*)(sSh + bo), bl = *(const h8*)(sSl + bo);
+                ksh = mfma32(ak, bh, ksh);
+                ksl = mfma32(ak, bl, ksl);
+                qsh = mfma32(aq, bh, qsh);
+                qsl = mfma32(aq, bl, qsl);
             }
+            // ---- X = V - e^G (K S) -> LDS as X^T [c][t] (hi, lo); lane: column lr,
+            //      tokens 16w + 4lg + r
+            f4 QS;
+            h4 xh, xl;
+            const float egr[4] = {C.eg.x, C.eg.y, C.eg.z, C.eg.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int t = n * kChunk + 16 * wave + 4 * lg + r;
-                if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + 16 * ct + lr] = acc[r] * a.scale;
+                const float vv = (C.vok >> r) & 1 ? (BF16 ? bf16_bits_to_f32(C.vw[r]) : __uint_as_float(C.vw[r])) : 0.0f;
+                const float x = vv - egr[r] * (ksh[r] + ksl[r]);
+                QS[r] = egr[r] * (qsh[r] + qsl[r]);
+                xh[r] = f16_hi(x), xl[r] = f16_lo(x);
             }
-        }
+            *(h4*)(sXh + lr * TP + 16 * wave + 4 * lg) = xh;
+            *(h4*)(sXl + lr * TP + 16 * wave + 4 * lg) = xl;
+            __syncthreads();
 
-        // ---- S = e^{G_C} S + K^T U' for this wave's state tiles
-        const float eGC = dec[128];
+            // ---- U = T X for token tile w; U and e^{G_C - G} U -> LDS as [c][t]
+            f4 u = f4{0.0f, 0.0f, 0.0f, 0.0f}, u2 = u;
 #pragma unroll
-        for (int a2 = 0; a2 < 2; ++a2) {
-            const int it = 2 * wave + a2;
+            for (int ks = 0; ks < 2; ++ks) {
+                const int bo = lr * TP + 32 * ks + 8 * lg;
+                const h8 bh = *(const h8*)(sXh + bo), bl = *(const h8*)(sXl + bo);
+                u = mfma32(C.th[ks], bh, u);
+                u2 = mfma32(C.th[ks], bl, u2);
+                u2 = mfma32(C.tl[ks], bh, u2);
+            }
+            u += u2;
+            {
+                const float egcr[4] = {C.egc.x, C.egc.y, C.egc.z, C.egc.w};
+                h4 uh, ul, wh, wl;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                f4 acc = S[a2][ct] * eGC;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const h4 ak = *(const h4*)(KT + (16 * it + lr) * 64 + 16 * ks + 4 * lg);
-                    const int bo = (16 * ct + lr) * UP + 16 * ks + 4 * lg;
-                    const h4 bh = *(const h4*)(sVh + bo), bl = *(const h4*)(sVl + bo);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ak, bh, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ak, bl, acc, 0, 0, 0);
+                for (int r = 0; r < 4; ++r) {
+                    const float w = u[r] * egcr[r];
+                    uh[r] = f16_hi(u[r]), ul[r] = f16_lo(u[r]);
+                    wh[r] = f16_hi(w), wl[r] = f16_lo(w);
                 }
-                S[a2][ct] = acc;
+                const int o = lr * TP + 16 * wave + 4 * lg;
+                *(h4*)(sUh + o) = uh;
+                *(h4*)(sUl + o) = ul;
+                *(h4*)(sWh + o) = wh;
+                *(h4*)(sWl + o) = wl;
+            }
+            __syncthreads();
+
+            // ---- Y = scale (e^G Q S + P U) for token tile w
+            f4 y = QS, y2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int bo = lr * TP + 32 * ks + 8 * lg;
+                const h8 bh = *(const h8*)(sUh + bo), bl = *(const h8*)(sUl + bo);
+                y = mfma32(C.ph[ks], bh, y);
+                y2 = mfma32(C.ph[ks], bl, y2);
+                y2 = mfma32(C.pl[ks], bh, y2);
+            }
+            y += y2;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = nn * kChunk + 16 * wave + 4 * lg + r;
+                if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * a.scale;
+            }
+
+            // ---- S = e^{G_C} S + K^T (e^{G_C - G} U) for this wave's key-dim tiles
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2) {
+                f4 acc = S[a2] * C.eGC, acc2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const int bo = lr * TP + 32 * ks + 8 * lg;
+                    acc = mfma32(C.kt[a2][ks], *(const h8*)(sWh + bo), acc);
+                    acc2 = mfma32(C.kt[a2][ks], *(const h8*)(sWl + bo), acc2);
+                }
+                S[a2] = acc + acc2;
             }
         }
     }
@@ -394,14 +529,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     // ---- final state (transposed layout: element (i, c) of head h at h*16384 + c*128 + i)
     float* so = a.state_out + (int64_t)b * (a.so_nb3 / 4) + (int64_t)h * 16384;
 #pragma unroll
-    for (int a2 = 0; a2 < 2; ++a2)
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int it = 2 * wave + a2;
-            const int c = kCols * cb + 16 * ct + lr;
-            *(float4*)(so + (int64_t)c * 128 + 16 * it + 4 * lg) =
-                make_float4(S[a2][ct][0], S[a2][ct][1], S[a2][ct][2], S[a2][ct][3]);
-        }
+    for (int a2 = 0; a2 < 2; ++a2) {
+        const int it = 2 * wave + a2;
+        *(float4*)(so + (int64_t)(kCols * cb + lr) * 128 + 16 * it + 4 * lg) =
+            make_float4(S[a2][0], S[a2][1], S[a2][2], S[a2][3]);
+    }
 }
 
 // ---------------------------------------------------------------- host
@@ -416,6 +548,18 @@ size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots) {
 }
 
 bool gdn_chunked_available() { return true; }
+
+template <bool BF16, bool VEC>
+static void chunked_kernels(const GdnChunkArgs& a, hipStream_t stream) {
+    {
+        ProfScope ps("gdn_chunk_prep", stream);
+        hipLaunchKernelGGL((gdn_chunk_prep<BF16, VEC>), dim3(a.n_chunks, 32, (uint32_t)a.B), dim3(256), 0, stream, a);
+    }
+    {
+        ProfScope ps("gdn_chunk_scan", stream);
+        hipLaunchKernelGGL((gdn_chunk_scan<BF16, VEC>), dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), 0, stream, a);
+    }
+}
 
 hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {
     const int64_t T = L.v->ne[2], B = L.v->ne[3];
@@ -444,18 +588,21 @@ hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {
     a.so_nb3 = L.dst->nb[2];
     a.T = (int32_t)Tc;
     a.n_chunks = (int32_t)((Tc + kChunk - 1) / kChunk);
+    a.B = (int32_t)B;
     a.scale = 1.0f / sqrtf(128.0f);
     const bool bf16 = L.q->type == XQ_TYPE_BF16;
-    {
-        ProfScope ps("gdn_chunk_prep", stream);
-        if (bf16)
-            hipLaunchKernelGGL(gdn_chunk_prep<true>, dim3(a.n_chunks, 32, (uint32_t)B), dim3(256), 0, stream, a);
-        else
-            hipLaunchKernelGGL(gdn_chunk_prep<false>, dim3(a.n_chunks, 32, (uint32_t)B), dim3(256), 0, stream, a);
+    // 16-byte row loads need 16-byte aligned q/k row bases
+    bool vec = true;
+    for (const xq_tensor* t : {L.q, L.k}) {
+        vec = vec && ((uintptr_t)t->data % 16 == 0);
+        for (int i = 1; i < 4; ++i) vec = vec && (t->nb[i] % 16 == 0);
     }
-    {
-        ProfScope ps("gdn_chunk_scan", stream);
-        hipLaunchKernelGGL(gdn_chunk_scan, dim3(128 / kCols, 32, (uint32_t)B), dim3(256), 0, stream, a);
+    if (bf16) {
+        if (vec) chunked_kernels<true, true>(a, stream);
+        else chunked_kernels<true, false>(a, stream);
+    } else {
+        if (vec) chunked_kernels<false, true>(a, stream);
+        else chunked_kernels<false, false>(a, stream);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || L.slots == 1) return e;
