@@ -273,14 +273,17 @@ def main():
                     help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
     ap.add_argument("--only", choices=["fa", "gdn", "prefill", "all"], default="all")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="write the traffic summary of fa_dec from two rocprofv3 --pmc output dirs and exit")
+                    help="write the traffic summary of --pmc-kernel from two rocprofv3 --pmc output dirs and exit")
+    ap.add_argument("--pmc-kernel", choices=["fa_dec", "gdn_step"], default="fa_dec",
+                    help="kernel of the --summarize-pmc summary (fa_dec: 32k q8_0 decode; gdn_step: 8-sequence step)")
     ap.add_argument("--pmc-command", action="append", default=[], help="command lines recorded in the summary")
     args = ap.parse_args()
     if args.summarize_pmc:
         from xqattn import workloads as wl
-        rec, text = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], "fa_dec", wl.FA_C2.name,
+        workload = {"fa_dec": wl.FA_C2.name, "gdn_step": wl.GDN_C3.name}[args.pmc_kernel]
+        rec, text = summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.pmc_kernel, workload,
                                   512 << 20, args.pmc_command)
-        out = ROOT / "profiles" / f"fa_dec_{wl.FA_C2.name}_traffic.md"
+        out = ROOT / "profiles" / f"{args.pmc_kernel}_{workload}_traffic.md"
         out.parent.mkdir(exist_ok=True)
         out.write_text(text)
         print(json.dumps(rec))
@@ -368,11 +371,17 @@ def main():
         g_alg = gcfg.algorithmic_bytes()
         g_kus = gkt.get("gdn_step", {}).get("avg_us", float("nan"))
         log(f"GDN: {g_ms * 1000:.2f} us/call, kernel {g_kus:.2f} us")
+        g_tr = traffic_from_profiles("gdn_step", gcfg.name)
+        # a call is one launch: the graph-replay time per call is the launch's
+        # duration plus the dispatch gap; the event pair around each eager launch
+        # adds more (it brackets the launch from the host)
         out["gdn_step"] = {"workload": gcfg.name, "us_per_call": round(g_ms * 1000, 3),
                            "kernel_avg_us": round(g_kus, 3), "algorithmic_bytes": g_alg,
                            "GB/s": round(g_alg / (g_kus * 1e-6) / 1e9, 1),
                            "frac": round(g_alg / (g_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
-                           "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "input_sets": g_sets_n}
+                           "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1),
+                           "call_frac": round(g_alg / (g_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                           "traffic": g_tr["traffic_bytes"] if g_tr else None, "input_sets": g_sets_n}
         if args.only == "gdn":
             out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})
