@@ -199,7 +199,8 @@ int64_t xq_fa_split_rows(int64_t kv_len, int32_t split_mode);
 enum xq_gdn_mode {
     XQ_GDN_AUTO = 0,     /* step for T <= 64, chunked above */
     XQ_GDN_STEP = 1,     /* token-sequential recurrence */
-    XQ_GDN_CHUNKED = 2,  /* chunked (C = 64) WY/UT form with bf16 MFMA */
+    XQ_GDN_CHUNKED = 2,  /* 64-token chunks in the UT form on the f16 matrix cores
+                            (f32 operands split into f16 hi + lo) */
 };
 
 /* Pure predicate mirroring d3d12_gdn_supported (src/bridge/ggml_d3d12.cpp:77-109),

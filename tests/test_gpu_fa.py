@@ -201,8 +201,8 @@ def test_fa_empty_trailing_split(torch_gpu, engine):
 
 
 def test_fa_graph_replays_match_eager(torch_gpu):
-    """A captured multi-split call replays bit-identically (the in-kernel split
-    merge leaves its arrival counters at zero after every call)."""
+    """A captured multi-split call (pass 1, then the split merge on the same
+    stream) replays bit-identically, with eager calls between the replays."""
     torch = torch_gpu
     cfg = wl.FaConfig("q8_graph", 1, 24, 4, 256, 6000, 2, wl.Q8_0)
     case_note("graph replays")
