@@ -130,6 +130,23 @@ def test_fa_predicate_and_workspace():
                                         ctypes.byref(p)) == 0
 
 
+def test_fa_workspace_reserves_mask_relayout():
+    """With a mask the workspace holds room for the mask rows re-laid with an
+    even element count ([n_q][mask heads][mask sequences] rows of f16, 256-byte
+    rounded), used when the rows are not 4-byte aligned."""
+    l = lib()
+    p = xqattn.fa_params(1.0 / 16)
+    for L, NQ, B in ((193, 1, 1), (1001, 4, 2), (32768, 1, 4)):
+        q, k, v, m, dst = _fa_descs(kv=wl.Q8_0, D=128, NQ=NQ, H=8, Hkv=2, L=L, B=B)
+        with_mask, without = ctypes.c_size_t(0), ctypes.c_size_t(0)
+        assert l.xq_flash_attn_ext_workspace(*(ctypes.byref(x) for x in (q, k, v, m)), None, ctypes.byref(dst),
+                                             ctypes.byref(p), ctypes.byref(with_mask)) == 0
+        assert l.xq_flash_attn_ext_workspace(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), None, None,
+                                             ctypes.byref(dst), ctypes.byref(p), ctypes.byref(without)) == 0
+        pack = B * NQ * (L + (L & 1)) * 2
+        assert with_mask.value - without.value == (pack + 255) // 256 * 256, (L, NQ, B)
+
+
 def test_fa_entry_rejects_before_any_device_work():
     l = lib()
     q, k, v, m, dst = _fa_descs()

@@ -186,6 +186,36 @@ def test_fa_range_vs_reference_semantics(torch_gpu, kv_type, active):
 
 
 @pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0])
+def test_fa_mask_rows_2byte_aligned(torch_gpu, kv_type, engine):
+    """An odd KV length gives mask rows of 2 (mod 4) bytes; a mask view may also
+    start 2 bytes into its buffer. Both run (the matrix-core engine re-lays such
+    a mask in the workspace first) and give the aligned layout's result."""
+    torch = torch_gpu
+    cfg = wl.FaConfig("odd", 4, 16, 4, 128, 1001, 2, kv_type, causal_prefix=997)
+    case_note(f"odd mask rows {wl.TYPE_NAME[kv_type]} engine {engine}")
+    case = make_fa_case(cfg, seed=41, mask_per_seq=True)
+    assert case.mask.nb[1] % 4 == 2
+    got, glse = run_gpu(case, torch, engine=engine)
+    want, _ = oracle_fa(case)
+    assert_close(got, want, what="odd-length mask vs ggml restatement")
+    ref64, lse64 = oracle_f64(case)
+    assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what="odd-length mask LSE")
+
+    cfg2 = wl.FaConfig("even", 4, 16, 4, 128, 1000, 2, kv_type, causal_prefix=996)
+    case2 = make_fa_case(cfg2, seed=43)
+    aligned, _ = run_gpu(case2, torch, engine=engine)
+    q, k, v = (xqattn.DevTensor.from_host(t) for t in (case2.q, case2.k, case2.v))
+    raw = np.concatenate([np.zeros(2, np.uint8), case2.mask.buf.reshape(-1)])
+    m = xqattn.DevTensor(case2.mask.type, case2.mask.ne, case2.mask.nb, torch.from_numpy(raw).cuda()[2:])
+    assert m.t.data_ptr() % 4 == 2
+    d = xqattn.DevTensor.empty_like_host(case2.dst)
+    xqattn.flash_attn_ext(q, k, v, m, None, d, xqattn.fa_params(case2.scale, engine=engine))
+    torch.cuda.synchronize()
+    assert np.array_equal(dst_array(case2, d.to_host_bytes()), aligned), "mask pointer offset changed the result"
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
 def test_fa_empty_trailing_split(torch_gpu, engine):
     """The reference's fine mode keeps 256 splits at 10200 rows (40 rows each), so
     the last split is empty; its partial state must merge as nothing."""

@@ -201,7 +201,8 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
         return fail(XQ_ERR_UNSUPPORTED, "no kernel for this combination");
     if (p->engine == XQ_FA_ENGINE_MFMA && !xq::fa_mma_available(P.kt, P.D, P.qk_mode, npairs))
         return fail(XQ_ERR_UNSUPPORTED, "no matrix-core kernel for this combination");
-    P.ws = xq::fa_workspace_bytes((int64_t)B * NQ * H, P.D, P.qk_mode, P.kt, P.n_splits);
+    P.ws = xq::fa_workspace_bytes((int64_t)B * NQ * H, P.D, P.qk_mode, P.kt, P.n_splits) +
+           xq::fa_mask_pack_bytes(mask, P.L, P.NQ);
     if (plan) *plan = P;
     return XQ_OK;
 }

@@ -14,6 +14,9 @@
 //               value phase gives each wave a quarter of the head dims and each
 //               16-lane row a quarter of the tile rows; partial (acc, m, l) per
 //               split, or the final output when there is a single split;
+//   fa_mask_pack — only for the matrix-core engine when the mask rows are not
+//               4-byte aligned (odd KV length): copies the mask rows the call
+//               reads into 4-byte aligned rows in the workspace;
 //   fa_reduce — merges the splits of one (sequence, query, head) in ascending
 //               split order (the consistent KV-reduction order of
 //               shaders/rkva/rkva_range_reduce.hlsl:12-46, with the non-finite
@@ -710,6 +713,31 @@ static size_t qimg_bytes(int64_t n_rows, int d, int qk_mode, int kt) {
     return (size_t)n_rows * qimg_words(qk_mode, kt, d) * 4;
 }
 
+// Mask rows re-laid with an even element count (4-byte aligned rows) for the
+// matrix-core engine: one row per (query, mask head plane, mask sequence
+// plane); the pad element is -inf.
+__host__ __device__ static inline int64_t mask_pack_cols(int64_t L) { return (L + 1) & ~(int64_t)1; }
+
+size_t fa_mask_pack_bytes(const xq_tensor* mask, int64_t L, int n_q) {
+    if (!mask) return 0;
+    return align256((size_t)mask->ne[3] * mask->ne[2] * n_q * mask_pack_cols(L) * 2);
+}
+
+__global__ __launch_bounds__(256) void fa_mask_pack(const uint8_t* __restrict__ src, int64_t nb1, int64_t nb2,
+                                                    int64_t nb3, int n_q, int ne2, int64_t L,
+                                                    uint32_t* __restrict__ dst) {
+    const int row = blockIdx.x;  // (b * ne2 + h) * n_q + q
+    const int qi = row % n_q, h = (row / n_q) % ne2, b = row / (n_q * ne2);
+    const uint16_t* s = (const uint16_t*)(src + qi * nb1 + h * nb2 + b * nb3);
+    const int64_t pairs = mask_pack_cols(L) / 2;
+    uint32_t* d = dst + row * pairs;
+    for (int64_t c = threadIdx.x; c < pairs; c += 256) {
+        const uint32_t lo = s[2 * c];
+        const uint32_t hi = 2 * c + 1 < L ? s[2 * c + 1] : 0xFC00u;
+        d[c] = lo | (hi << 16);
+    }
+}
+
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits) {
     size_t bytes = align256(qimg_bytes(n_rows, d, qk_mode, kt));
     if (n_splits > 1) {
@@ -791,9 +819,26 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
         a.part_ml = (float2*)(ws + off);
     }
 
-    const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G) && fa_mma_mask_ok(a);
+    const bool mma = L.engine != XQ_FA_ENGINE_VALU && fa_mma_available(kt, D, L.qk_mode, QT * G);
     if (L.engine == XQ_FA_ENGINE_MFMA && !mma) return hipErrorInvalidValue;
-    if (mma) return fa_mma_launch(a, L, stream);
+    if (mma) {
+        if (!fa_mma_mask_ok(a)) {
+            const size_t base = fa_workspace_bytes(n_rows, D, L.qk_mode, kt, L.n_splits);
+            if (L.workspace_bytes < base + fa_mask_pack_bytes(L.mask, a.L, NQ)) return hipErrorInvalidValue;
+            uint32_t* packed = (uint32_t*)(ws + base);
+            const int n_pack = NQ * a.m_ne2 * a.m_ne3;
+            {
+                ProfScope ps("fa_mask_pack", stream);
+                hipLaunchKernelGGL(fa_mask_pack, dim3((uint32_t)n_pack), dim3(256), 0, stream, a.mask, a.m_nb1,
+                                   a.m_nb2, a.m_nb3, NQ, a.m_ne2, a.L, packed);
+            }
+            a.mask = (const uint8_t*)packed;
+            a.m_nb1 = mask_pack_cols(a.L) * 2;
+            a.m_nb2 = (int64_t)NQ * a.m_nb1;
+            a.m_nb3 = (int64_t)a.m_ne2 * a.m_nb2;
+        }
+        return fa_mma_launch(a, L, stream);
+    }
     Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);
     QprepFn qp = D == 128 ? qprep_d<128>(kt, L.qk_mode) : qprep_d<256>(kt, L.qk_mode);
     if (!p1 || !qp) return hipErrorInvalidValue;

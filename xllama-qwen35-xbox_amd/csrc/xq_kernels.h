@@ -76,6 +76,9 @@ struct FaLaunch {
 };
 
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits);
+// Extra workspace after fa_workspace_bytes for a mask whose rows the
+// matrix-core engine must re-lay (reserved whenever a mask is given).
+size_t fa_mask_pack_bytes(const xq_tensor* mask, int64_t L, int n_q);
 hipError_t fa_launch(const FaLaunch& L, hipStream_t stream);
 // Whether a compiled kernel exists for this combination.
 bool fa_kernel_available(int kt, int d, int qk_mode, int n_pairs);
