@@ -46,6 +46,7 @@ GDN_CASES = [
     ("gdn_step_b2", 1, 2, 1, False, list(range(32)), [0, 5, 17, 31], list(range(0, 128, 8))),
     ("gdn_snapshots_t5", 5, 1, 3, False, list(range(32)), [3, 20], list(range(0, 128, 8))),
     ("gdn_chunked_t130_bf16", 130, 1, 1, True, [0, 13, 31], [0, 17, 31], list(range(0, 128, 4))),
+    ("gdn_chunked_t136_f32_fine", 136, 1, 2, False, [2, 30], [6, 25], list(range(0, 128, 4))),
 ]
 
 
@@ -113,9 +114,11 @@ def kv_store_fixture(seed):
 
 
 def gdn_fixture(name, T, B, slots, bf16, y_heads, st_heads, st_cols, seed):
+    fine = name.endswith("_fine")
     meta = dict(kind="gdn", T=T, B=B, slots=slots, bf16=bf16, seed=seed, y_heads=y_heads,
-                state_heads=st_heads, state_cols=st_cols,
-                recipe="q,k = c/1024, v = c/64, g = -(c+129)/4096, beta = (c+128)/256, state = c/256")
+                state_heads=st_heads, state_cols=st_cols, fine=fine,
+                recipe=("q,k = c16/2^18" if fine else "q,k = c/1024") +
+                ", v = c/64, g = -(c+129)/4096, beta = (c+128)/256, state = c/256")
     (q, k, v, g, beta, st, dst), hashes = gio.gdn_tensors(meta)
     meta["sha256"] = hashes
     oracle.gated_delta_net(q, k, v, g, beta, st, dst, slots, 8)

@@ -72,13 +72,23 @@ def int_codes(seed: int, n: int) -> np.ndarray:
     return (wl.splitmix64(seed, n) >> np.uint64(56)).astype(np.int64) - 128
 
 
-def gdn_coded_inputs(seed: int, T: int, B: int):
+def gdn_coded_inputs(seed: int, T: int, B: int, fine: bool = False):
     """q, k = c/1024, v = c/64, g = -(c+129)/4096 (in [-1/16, 0)), beta = (c+128)/256,
-    state = c/256, each c from its own stream. Exact in f32 and in bf16."""
+    state = c/256, each c from its own stream. Exact in f32 and in bf16.
+    fine: q, k = c16/2^18 with c16 = 256 c + c' (16-bit codes, same range), exact
+    in f32 but not in f16 or bf16."""
     def codes(j, shape, s):
         return (int_codes(seed + j, int(np.prod(shape))) * s).astype(np.float32).reshape(shape)
-    q = codes(1, (B, T, 16, 128), 2.0 ** -10)
-    k = codes(2, (B, T, 16, 128), 2.0 ** -10)
+    if fine:
+        def codes16(j, shape):
+            n = int(np.prod(shape))
+            c = int_codes(seed + j, n) * 256 + int_codes(seed + 100 + j, n) + 128
+            return (c * 2.0 ** -18).astype(np.float32).reshape(shape)
+        q = codes16(1, (B, T, 16, 128))
+        k = codes16(2, (B, T, 16, 128))
+    else:
+        q = codes(1, (B, T, 16, 128), 2.0 ** -10)
+        k = codes(2, (B, T, 16, 128), 2.0 ** -10)
     v = codes(3, (B, T, 32, 128), 2.0 ** -6)
     g = (-(int_codes(seed + 4, B * T * 32) + 129) * 2.0 ** -12).astype(np.float32).reshape(B, T, 32)
     beta = ((int_codes(seed + 5, B * T * 32) + 128) * 2.0 ** -8).astype(np.float32).reshape(B, T, 32)
@@ -90,7 +100,7 @@ def gdn_tensors(meta: dict, pad: int = 0):
     """Host tensors (q, k, v, g, beta, state, dst) of a coded GDN fixture; dst
     filled with a sentinel. Rows of q, k, v may be padded (layout only)."""
     T, B, slots, bf16 = meta["T"], meta["B"], meta["slots"], meta["bf16"]
-    q, k, v, g, beta, st = gdn_coded_inputs(meta["seed"], T, B)
+    q, k, v, g, beta, st = gdn_coded_inputs(meta["seed"], T, B, meta.get("fine", False))
     typ = wl.BF16 if bf16 else wl.F32
     if bf16:  # the codes are exact in bf16: keep the top half of each f32
         q, k, v = ((a.view(np.uint32) >> np.uint32(16)).astype(np.uint16) for a in (q, k, v))

@@ -180,18 +180,21 @@ def test_gdn_predicate():
 
 def test_gdn_workspace_query():
     """AUTO runs prefills longer than one chunk on the chunked kernels: one
-    workspace record of 50176 bytes per (sequence, v-head, 64-token chunk) of
-    the first T - (slots - 1) tokens; the step kernel needs none."""
+    workspace record of 50176 bytes (66560 for f32 rows) per (sequence,
+    v-head, 64-token chunk) of the first T - (slots - 1) tokens; the step
+    kernel needs none."""
     l = lib()
     n = ctypes.c_size_t(0)
 
-    def need(T, B, slots, mode):
-        q = _desc(wl.BF16, (128, 16, T, B))
-        v = _desc(wl.BF16, (128, 32, T, B))
+    def need(T, B, slots, mode, typ=wl.BF16):
+        q = _desc(typ, (128, 16, T, B))
+        v = _desc(typ, (128, 32, T, B))
         assert l.xq_gated_delta_net_workspace(ctypes.byref(q), ctypes.byref(v), slots, mode, ctypes.byref(n)) == 0
         return n.value
 
     rec = 4 * 64 * 64 * 2 + 128 * 64 * 2 + 1024  # T, P (f16 hi, lo), K^T (f16), decays
+    # f32 rows also keep the f16 remainder of K^T
+    assert need(4096, 1, 1, xqattn.GDN_AUTO, wl.F32) == 32 * 64 * (rec + 128 * 64 * 2)
     assert need(200, 2, 3, xqattn.GDN_CHUNKED) == 2 * 32 * 4 * rec  # 198 tokens -> 4 chunks
     assert need(4096, 1, 1, xqattn.GDN_AUTO) == 32 * 64 * rec
     assert need(64, 1, 1, xqattn.GDN_AUTO) == 0                     # one chunk: step kernel

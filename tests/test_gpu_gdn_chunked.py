@@ -81,6 +81,22 @@ def test_gdn_chunked_matches_step_kernel(torch_gpu):
     _check(case, c, a, "chunked vs step kernel")
 
 
+@pytest.mark.parametrize("bf16", [True, False])
+def test_gdn_chunked_meets_reference_selftest_bar(torch_gpu, bf16):
+    """max|gpu - want| / max|want| <= 1e-4 over the outputs and the state, the
+    reference selftest's criterion (src/bridge/ggml_d3d12.cpp:285-301), against
+    the float64 recurrence, at 300 tokens (4 full chunks + tail). f32 rows
+    enter the matrix products as f16 hi + lo, bf16 rows exactly."""
+    case_note(f"gdn chunked selftest bar bf16={bf16}")
+    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=bf16, seed=99)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    want = case.oracle_f64()
+    v = _valid_rows(case)
+    rel = np.abs(got[:, :v] - want[:, :v]).max() / np.abs(want[:, :v]).max()
+    print(f"bf16={bf16}: rel {rel:.2e}")
+    assert rel <= 1e-4, rel
+
+
 def test_gdn_chunked_strong_decay(torch_gpu):
     """Decays that underflow within a chunk (g = -40 per token) keep every
     factor in [0, 1] and the result finite."""

@@ -429,7 +429,9 @@ xq_status xq_gated_delta_net_workspace(const xq_tensor* q, const xq_tensor* v, i
     if (!q || !v || !bytes) return fail(XQ_ERR_BAD_ARG, "null argument");
     if (mode < XQ_GDN_AUTO || mode > XQ_GDN_CHUNKED) return fail(XQ_ERR_BAD_ARG, "bad mode");
     const int64_t T = v->ne[2], B = v->ne[3];
-    *bytes = gdn_pick(mode, T) == XQ_GDN_CHUNKED ? xq::gdn_chunked_workspace_bytes(T, B, slots) : 0;
+    *bytes = gdn_pick(mode, T) == XQ_GDN_CHUNKED
+                 ? xq::gdn_chunked_workspace_bytes(T, B, slots, q->type == XQ_TYPE_BF16)
+                 : 0;
     return ok();
 }
 
@@ -450,7 +452,7 @@ xq_status xq_gated_delta_net(const xq_tensor* q, const xq_tensor* k, const xq_te
     const int64_t T = v->ne[2], B = v->ne[3];
     hipError_t e;
     if (gdn_pick(mode, T) == XQ_GDN_CHUNKED) {
-        const size_t need = xq::gdn_chunked_workspace_bytes(T, B, slots);
+        const size_t need = xq::gdn_chunked_workspace_bytes(T, B, slots, q->type == XQ_TYPE_BF16);
         if (need && (!workspace || workspace_bytes < need))
             return fail(XQ_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, workspace_bytes);
         e = xq::gdn_chunked_launch(L, (hipStream_t)stream);

@@ -21,11 +21,15 @@
 //                   the unit lower-triangular solve for T in f32, P with its
 //                   decays; stores T and P as f16 hi + lo planes, K^T as f16
 //                   and the decay vectors (49 KB per chunk) in the workspace.
+//                   f32 q / k rows enter as f16 hi + lo (the products take
+//                   hi*hi + hi*lo + lo*hi) and the record also keeps K^T lo
+//                   (65 KB); bf16 rows are f16 values already (their 8
+//                   significant bits fit, down to 2^-24).
 //   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
 //                   the chunks in order with its 128 x 16 state block in
 //                   registers (f32). Every MFMA operand that does not depend on
-//                   the state (K and Q rows straight from the inputs, as f16:
-//                   exact for bf16 rows; K^T, T and P rows from the workspace;
+//                   the state (K and Q rows straight from the inputs, as f16,
+//                   or f16 hi + lo for f32 rows; K^T, T and P rows from the workspace;
 //                   V and the decays) is loaded into registers a chunk ahead;
 //                   LDS carries only the state-dependent exchanges (S^T, X^T,
 //                   U^T). The products run on v_mfma_f32_16x16x32_f16 with f32
@@ -52,7 +56,9 @@ constexpr int kRecPHi = kRecTLo + 64 * 64 * 2;  // f16 [64][64]
 constexpr int kRecPLo = kRecPHi + 64 * 64 * 2;
 constexpr int kRecKT = kRecPLo + 64 * 64 * 2;  // f16 K^T [128][64]
 constexpr int kRecDec = kRecKT + 128 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}
-constexpr int kRecBytes = kRecDec + 1024;
+constexpr int kRecKTLo = kRecDec + 1024;        // f32 rows only: f16 K^T lo [128][64]
+template <bool BF16>
+constexpr int rec_bytes() { return BF16 ? kRecKTLo : kRecKTLo + 128 * 64 * 2; }
 
 struct GdnChunkArgs {
     const uint8_t* q;
@@ -111,6 +117,14 @@ XQ_DEV h8 to_h8(const float (&x)[8]) {
     return r;
 }
 
+// the f16 remainders x - hi of eight values whose f16 parts are hi
+XQ_DEV h8 lo_h8(const float (&x)[8], h8 hi) {
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)(x[e] - (float)hi[e]);
+    return r;
+}
+
 XQ_DEV f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
 // ---------------------------------------------------------------- prep
@@ -120,13 +134,16 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
     constexpr int KP = 136;  // padded f16 row stride (halves)
     constexpr int TP = 72;   // K^T row stride (halves)
     constexpr int FP = 65;   // padded f32 row stride
-    // 68.6 KB: two workgroups per CU. sKT holds K^T for the record; after the
+    // 68.6 KB for bf16 rows: two workgroups per CU. sKT holds K^T for the record; after the
     // products sK becomes T and sQ the P planes.
     __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][65]
     __shared__ __attribute__((aligned(16))) _Float16 sKT[128 * TP];  // K^T [i][t]
     __shared__ __attribute__((aligned(16))) _Float16 sQ[64 * KP];    // Q [t][i], then P hi, lo [64][64]
     __shared__ float sKK[64 * FP];  // K K^T, then L
     __shared__ float sG[64], sBeta[64], sEG[64];
+    // f32 rows: the f16 remainders of K, K^T and Q (+52 KB: one workgroup per CU)
+    constexpr int NKL = BF16 ? 8 : 64 * KP, NKTL = BF16 ? 8 : 128 * TP;
+    __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL], sKTl[NKTL], sQl[NKL];
     static_assert(64 * FP * 4 <= 64 * KP * 2 && 2 * 64 * 64 * 2 <= 64 * KP * 2, "LDS aliases");
 
     const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -154,11 +171,18 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) xk[e] = xq[e] = 0.0f;
             }
-            const h8 hk = to_h8(xk);
+            const h8 hk = to_h8(xk), hq = to_h8(xq);
             *(h8*)(sK + t * KP + i0) = hk;
-            *(h8*)(sQ + t * KP + i0) = to_h8(xq);
+            *(h8*)(sQ + t * KP + i0) = hq;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sKT[(i0 + e) * TP + t] = hk[e];
+            if constexpr (!BF16) {
+                const h8 lk = lo_h8(xk, hk);
+                *(h8*)(sKl + t * KP + i0) = lk;
+                *(h8*)(sQl + t * KP + i0) = lo_h8(xq, hq);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) sKTl[(i0 + e) * TP + t] = lk[e];
+            }
         }
         if (tid < 64) {
             const int tt = t0 + tid;
@@ -189,6 +213,15 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
             const h8 aq = *(const h8*)(sQ + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
             kk = mfma32(ak, bk, kk);
             qk[tt] = mfma32(aq, bk, qk[tt]);
+            if constexpr (!BF16) {
+                const h8 bkl = *(const h8*)(sKl + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
+                const h8 akl = *(const h8*)(sKl + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
+                const h8 aql = *(const h8*)(sQl + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
+                kk = mfma32(ak, bkl, kk);
+                kk = mfma32(akl, bk, kk);
+                qk[tt] = mfma32(aq, bkl, qk[tt]);
+                qk[tt] = mfma32(aql, bk, qk[tt]);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) sKK[(mt * 16 + 4 * lg + r) * FP + nt * 16 + lr] = kk[r];
@@ -248,7 +281,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
 
     // ---- the record: T (f16 hi + lo), P (hi, lo), K^T (f16) with 16-byte
     //      stores, and the decays
-    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
     {
         const int t = tid >> 2, j0 = 16 * (tid & 3);
         h8 th[2], tl[2];
@@ -270,6 +303,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
     for (int u = 0; u < 4; ++u) {  // K^T: 1024 chunks of 8 tokens
         const int e = tid + 256 * u, i = e >> 3, c8 = e & 7;
         *(h8*)(rec + kRecKT + (i * 64 + 8 * c8) * 2) = *(const h8*)(sKT + i * TP + 8 * c8);
+        if constexpr (!BF16)
+            *(h8*)(rec + kRecKTLo + (i * 64 + 8 * c8) * 2) = *(const h8*)(sKTl + i * TP + 8 * c8);
     }
     if (tid < 64) {
         const float GC = sEG[63];
@@ -296,6 +331,7 @@ struct ScanOps {
     static constexpr int KW = VEC ? (BF16 ? 1 : 2) : 4;  // 16-byte words per 8 elements (VEC), else raw dwords
     uint4 kw[4][KW], qw[4][KW];
     h8 th[2], tl[2], ph[2], pl[2], kt[2][2];
+    h8 ktl[BF16 ? 1 : 2][2];  // K^T lo (f32 rows)
     uint32_t vw[4];
     float4 eg, egc;
     float eGC;
@@ -319,6 +355,19 @@ XQ_DEV void load_raw8(const uint8_t* row, int i0, uint4 (&w)[KW]) {
         w[1] = make_uint4(e[4], e[5], e[6], e[7]);
         w[2] = w[3] = make_uint4(0, 0, 0, 0);
     }
+}
+
+// f32 rows: the f16 remainder x - f16(x) of the same eight elements
+template <int KW>
+XQ_DEV h8 decode8_lo(const uint4 (&w)[KW], bool ok) {
+    const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = __uint_as_float(u[e]);
+        r[e] = ok ? (_Float16)(x - (float)(_Float16)x) : (_Float16)0.0f;
+    }
+    return r;
 }
 
 template <bool BF16, bool VEC, int KW>
@@ -359,7 +408,7 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
             load_raw8<BF16, VEC>(qr, 32 * ks + 8 * lg, L.qw[ks]);
         }
     }
-    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
         const int o = ((16 * wave + lr) * 64 + 32 * ks + 8 * lg) * 2;
@@ -368,8 +417,11 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
         L.ph[ks] = *(const h8*)(rec + kRecPHi + o);
         L.pl[ks] = *(const h8*)(rec + kRecPLo + o);
 #pragma unroll
-        for (int a2 = 0; a2 < 2; ++a2)
-            L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2);
+        for (int a2 = 0; a2 < 2; ++a2) {
+            const int ko = ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2;
+            L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ko);
+            if constexpr (!BF16) L.ktl[a2][ks] = *(const h8*)(rec + kRecKTLo + ko);
+        }
     }
     const float* dec = (const float*)(rec + kRecDec);
     L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
@@ -449,6 +501,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
                 ksl = mfma32(ak, bl, ksl);
                 qsh = mfma32(aq, bh, qsh);
                 qsl = mfma32(aq, bl, qsl);
+                if constexpr (!BF16) {
+                    ksl = mfma32(decode8_lo(C.kw[ks], C.ok), bh, ksl);
+                    qsl = mfma32(decode8_lo(C.qw[ks], C.ok), bh, qsl);
+                }
             }
             // ---- X = V - e^G (K S) -> LDS as X^T [c][t] (hi, lo); lane: column lr,
             //      tokens 16w + 4lg + r
@@ -518,8 +574,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
                     const int bo = lr * TP + 32 * ks + 8 * lg;
-                    acc = mfma32(C.kt[a2][ks], *(const h8*)(sWh + bo), acc);
+                    const h8 wh = *(const h8*)(sWh + bo);
+                    acc = mfma32(C.kt[a2][ks], wh, acc);
                     acc2 = mfma32(C.kt[a2][ks], *(const h8*)(sWl + bo), acc2);
+                    if constexpr (!BF16) acc2 = mfma32(C.ktl[a2][ks], wh, acc2);
                 }
                 S[a2] = acc + acc2;
             }
@@ -540,11 +598,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 
 static int64_t chunked_tokens(int64_t T, int32_t slots) { return slots > 1 ? T - (slots - 1) : T; }
 
-size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots) {
+size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots, bool bf16_rows) {
     const int64_t Tc = chunked_tokens(T, slots);
     if (Tc < 1) return 0;
     const int64_t nch = (Tc + kChunk - 1) / kChunk;
-    return (size_t)B * 32 * nch * kRecBytes;
+    return (size_t)B * 32 * nch * (bf16_rows ? rec_bytes<true>() : rec_bytes<false>());
 }
 
 bool gdn_chunked_available() { return true; }
@@ -565,7 +623,8 @@ hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {
     const int64_t T = L.v->ne[2], B = L.v->ne[3];
     const int64_t Tc = chunked_tokens(T, L.slots);
     if (Tc < 1) return gdn_step_launch(L, stream);  // every token needs its own snapshot
-    if (L.workspace_bytes < gdn_chunked_workspace_bytes(T, B, L.slots)) return hipErrorInvalidValue;
+    if (L.workspace_bytes < gdn_chunked_workspace_bytes(T, B, L.slots, L.q->type == XQ_TYPE_BF16))
+        return hipErrorInvalidValue;
     GdnChunkArgs a{};
     a.q = (const uint8_t*)L.q->data;
     a.k = (const uint8_t*)L.k->data;

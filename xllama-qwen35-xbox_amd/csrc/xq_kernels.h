@@ -102,7 +102,7 @@ struct GdnLaunch {
 hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream);
 // Chunked prefill: tokens [0, T - (slots - 1)) in 64-token chunks, the last
 // slots - 1 tokens on the step kernel so each keeps its snapshot.
-size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots);
+size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots, bool bf16_rows);
 hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream);
 bool gdn_chunked_available();
 
