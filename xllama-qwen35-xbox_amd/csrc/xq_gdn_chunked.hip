@@ -37,6 +37,8 @@
 //                   so the result stays within f32-recurrence tolerances.
 // The 8 column blocks of a head run on one XCD (consecutive logical workgroups)
 // so the chunk rows and T, P they share are read from HBM once.
+#include <type_traits>
+
 #include "xq_kernels.h"
 
 namespace xq {
@@ -332,7 +334,9 @@ struct ScanOps {
     uint4 kw[4][KW], qw[4][KW];
     h8 th[2], tl[2], ph[2], pl[2], kt[2][2];
     h8 ktl[BF16 ? 1 : 2][2];  // K^T lo (f32 rows)
-    uint32_t vw[4];
+    // raw V words, in the input's width: a 16-bit load widened at use (widened
+    // here, the compiler copies the value at the loop edge and waits for it)
+    std::conditional_t<BF16, uint16_t, uint32_t> vw[4];
     float4 eg, egc;
     float eGC;
     bool ok;        // the A-operand token is in range
@@ -435,7 +439,10 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
         const int tc = min(tg, a.T - 1);
         const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tc * a.v_nb2 + (int64_t)h * a.v_nb1;
         const int c = kCols * cb + lr;
-        L.vw[r] = BF16 ? (uint32_t)((const uint16_t*)vr)[c] : ((const uint32_t*)vr)[c];
+        if constexpr (BF16)
+            L.vw[r] = ((const uint16_t*)vr)[c];
+        else
+            L.vw[r] = ((const uint32_t*)vr)[c];
     }
 }
 
@@ -469,120 +476,125 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 
     ScanOps<BF16, VEC> ops[2];
     scan_load<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
-    for (int n = 0; n < a.n_chunks; n += 2) {
-        // two chunks per iteration so the operand sets stay in fixed registers
-#pragma unroll
-        for (int par = 0; par < 2; ++par) {
-            const int nn = n + par;
-            if (nn >= a.n_chunks) break;
-            ScanOps<BF16, VEC>& C = ops[par];
-            scan_load<BF16, VEC>(a, b, h, cb, nn + 1, wave, lr, lg, ops[par ^ 1]);
+    // One chunk: C holds its operands (loaded a chunk ahead), the next chunk's
+    // operands are loaded into Nx.
+    auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx) {
+        scan_load<BF16, VEC>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
 
-            // ---- S (hi, lo) -> LDS as S^T [c][i]: the B operand rows of K S and Q S
+        // ---- S (hi, lo) -> LDS as S^T [c][i]: the B operand rows of K S and Q S
 #pragma unroll
-            for (int a2 = 0; a2 < 2; ++a2) {
-                const int it = 2 * wave + a2;
-                h4 sh, sl;
+        for (int a2 = 0; a2 < 2; ++a2) {
+            const int it = 2 * wave + a2;
+            h4 sh, sl;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) sh[r] = f16_hi(S[a2][r]), sl[r] = f16_lo(S[a2][r]);
-                *(h4*)(sSh + lr * SP + 16 * it + 4 * lg) = sh;
-                *(h4*)(sSl + lr * SP + 16 * it + 4 * lg) = sl;
-            }
-            __syncthreads();
+            for (int r = 0; r < 4; ++r) sh[r] = f16_hi(S[a2][r]), sl[r] = f16_lo(S[a2][r]);
+            *(h4*)(sSh + lr * SP + 16 * it + 4 * lg) = sh;
+            *(h4*)(sSl + lr * SP + 16 * it + 4 * lg) = sl;
+        }
+        __syncthreads();
 
-            // ---- K S and Q S for token tile w (16 tokens x 16 columns)
-            f4 ksh = f4{0.0f, 0.0f, 0.0f, 0.0f}, ksl = ksh, qsh = ksh, qsl = ksh;
+        // ---- K S and Q S for token tile w (16 tokens x 16 columns)
+        f4 ksh = f4{0.0f, 0.0f, 0.0f, 0.0f}, ksl = ksh, qsh = ksh, qsl = ksh;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const h8 ak = decode8<BF16, VEC>(C.kw[ks], C.ok), aq = decode8<BF16, VEC>(C.qw[ks], C.ok);
-                const int bo = lr * SP + 32 * ks + 8 * lg;
-                const h8 bh = *(const h8*)(sSh + bo), bl = *(const h8*)(sSl + bo);
-                ksh = mfma32(ak, bh, ksh);
-                ksl = mfma32(ak, bl, ksl);
-                qsh = mfma32(aq, bh, qsh);
-                qsl = mfma32(aq, bl, qsl);
-                if constexpr (!BF16) {
-                    ksl = mfma32(decode8_lo(C.kw[ks], C.ok), bh, ksl);
-                    qsl = mfma32(decode8_lo(C.qw[ks], C.ok), bh, qsl);
-                }
-            }
-            // ---- X = V - e^G (K S) -> LDS as X^T [c][t] (hi, lo); lane: column lr,
-            //      tokens 16w + 4lg + r
-            f4 QS;
-            h4 xh, xl;
-            const float egr[4] = {C.eg.x, C.eg.y, C.eg.z, C.eg.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float vv = (C.vok >> r) & 1 ? (BF16 ? bf16_bits_to_f32(C.vw[r]) : __uint_as_float(C.vw[r])) : 0.0f;
-                const float x = vv - egr[r] * (ksh[r] + ksl[r]);
-                QS[r] = egr[r] * (qsh[r] + qsl[r]);
-                xh[r] = f16_hi(x), xl[r] = f16_lo(x);
-            }
-            *(h4*)(sXh + lr * TP + 16 * wave + 4 * lg) = xh;
-            *(h4*)(sXl + lr * TP + 16 * wave + 4 * lg) = xl;
-            __syncthreads();
-
-            // ---- U = T X for token tile w; U and e^{G_C - G} U -> LDS as [c][t]
-            f4 u = f4{0.0f, 0.0f, 0.0f, 0.0f}, u2 = u;
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int bo = lr * TP + 32 * ks + 8 * lg;
-                const h8 bh = *(const h8*)(sXh + bo), bl = *(const h8*)(sXl + bo);
-                u = mfma32(C.th[ks], bh, u);
-                u2 = mfma32(C.th[ks], bl, u2);
-                u2 = mfma32(C.tl[ks], bh, u2);
-            }
-            u += u2;
-            {
-                const float egcr[4] = {C.egc.x, C.egc.y, C.egc.z, C.egc.w};
-                h4 uh, ul, wh, wl;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float w = u[r] * egcr[r];
-                    uh[r] = f16_hi(u[r]), ul[r] = f16_lo(u[r]);
-                    wh[r] = f16_hi(w), wl[r] = f16_lo(w);
-                }
-                const int o = lr * TP + 16 * wave + 4 * lg;
-                *(h4*)(sUh + o) = uh;
-                *(h4*)(sUl + o) = ul;
-                *(h4*)(sWh + o) = wh;
-                *(h4*)(sWl + o) = wl;
-            }
-            __syncthreads();
-
-            // ---- Y = scale (e^G Q S + P U) for token tile w
-            f4 y = QS, y2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int bo = lr * TP + 32 * ks + 8 * lg;
-                const h8 bh = *(const h8*)(sUh + bo), bl = *(const h8*)(sUl + bo);
-                y = mfma32(C.ph[ks], bh, y);
-                y2 = mfma32(C.ph[ks], bl, y2);
-                y2 = mfma32(C.pl[ks], bh, y2);
-            }
-            y += y2;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = nn * kChunk + 16 * wave + 4 * lg + r;
-                if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * a.scale;
-            }
-
-            // ---- S = e^{G_C} S + K^T (e^{G_C - G} U) for this wave's key-dim tiles
-#pragma unroll
-            for (int a2 = 0; a2 < 2; ++a2) {
-                f4 acc = S[a2] * C.eGC, acc2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const int bo = lr * TP + 32 * ks + 8 * lg;
-                    const h8 wh = *(const h8*)(sWh + bo);
-                    acc = mfma32(C.kt[a2][ks], wh, acc);
-                    acc2 = mfma32(C.kt[a2][ks], *(const h8*)(sWl + bo), acc2);
-                    if constexpr (!BF16) acc2 = mfma32(C.ktl[a2][ks], wh, acc2);
-                }
-                S[a2] = acc + acc2;
+        for (int ks = 0; ks < 4; ++ks) {
+            const h8 ak = decode8<BF16, VEC>(C.kw[ks], C.ok), aq = decode8<BF16, VEC>(C.qw[ks], C.ok);
+            const int bo = lr * SP + 32 * ks + 8 * lg;
+            const h8 bh = *(const h8*)(sSh + bo), bl = *(const h8*)(sSl + bo);
+            ksh = mfma32(ak, bh, ksh);
+            ksl = mfma32(ak, bl, ksl);
+            qsh = mfma32(aq, bh, qsh);
+            qsl = mfma32(aq, bl, qsl);
+            if constexpr (!BF16) {
+                ksl = mfma32(decode8_lo(C.kw[ks], C.ok), bh, ksl);
+                qsl = mfma32(decode8_lo(C.qw[ks], C.ok), bh, qsl);
             }
         }
+        // ---- X = V - e^G (K S) -> LDS as X^T [c][t] (hi, lo); lane: column lr,
+        //      tokens 16w + 4lg + r
+        f4 QS;
+        h4 xh, xl;
+        const float egr[4] = {C.eg.x, C.eg.y, C.eg.z, C.eg.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float vv = (C.vok >> r) & 1 ? (BF16 ? bf16_bits_to_f32(C.vw[r]) : __uint_as_float(C.vw[r])) : 0.0f;
+            const float x = vv - egr[r] * (ksh[r] + ksl[r]);
+            QS[r] = egr[r] * (qsh[r] + qsl[r]);
+            xh[r] = f16_hi(x), xl[r] = f16_lo(x);
+        }
+        *(h4*)(sXh + lr * TP + 16 * wave + 4 * lg) = xh;
+        *(h4*)(sXl + lr * TP + 16 * wave + 4 * lg) = xl;
+        __syncthreads();
+
+        // ---- U = T X for token tile w; U and e^{G_C - G} U -> LDS as [c][t]
+        f4 u = f4{0.0f, 0.0f, 0.0f, 0.0f}, u2 = u;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int bo = lr * TP + 32 * ks + 8 * lg;
+            const h8 bh = *(const h8*)(sXh + bo), bl = *(const h8*)(sXl + bo);
+            u = mfma32(C.th[ks], bh, u);
+            u2 = mfma32(C.th[ks], bl, u2);
+            u2 = mfma32(C.tl[ks], bh, u2);
+        }
+        u += u2;
+        {
+            const float egcr[4] = {C.egc.x, C.egc.y, C.egc.z, C.egc.w};
+            h4 uh, ul, wh, wl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float w = u[r] * egcr[r];
+                uh[r] = f16_hi(u[r]), ul[r] = f16_lo(u[r]);
+                wh[r] = f16_hi(w), wl[r] = f16_lo(w);
+            }
+            const int o = lr * TP + 16 * wave + 4 * lg;
+            *(h4*)(sUh + o) = uh;
+            *(h4*)(sUl + o) = ul;
+            *(h4*)(sWh + o) = wh;
+            *(h4*)(sWl + o) = wl;
+        }
+        __syncthreads();
+
+        // ---- Y = scale (e^G Q S + P U) for token tile w
+        f4 y = QS, y2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int bo = lr * TP + 32 * ks + 8 * lg;
+            const h8 bh = *(const h8*)(sUh + bo), bl = *(const h8*)(sUl + bo);
+            y = mfma32(C.ph[ks], bh, y);
+            y2 = mfma32(C.ph[ks], bl, y2);
+            y2 = mfma32(C.pl[ks], bh, y2);
+        }
+        y += y2;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = nn * kChunk + 16 * wave + 4 * lg + r;
+            if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * a.scale;
+        }
+
+        // ---- S = e^{G_C} S + K^T (e^{G_C - G} U) for this wave's key-dim tiles
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2) {
+            f4 acc = S[a2] * C.eGC, acc2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int bo = lr * TP + 32 * ks + 8 * lg;
+                const h8 wh = *(const h8*)(sWh + bo);
+                acc = mfma32(C.kt[a2][ks], wh, acc);
+                acc2 = mfma32(C.kt[a2][ks], *(const h8*)(sWl + bo), acc2);
+                if constexpr (!BF16) acc2 = mfma32(C.ktl[a2][ks], wh, acc2);
+            }
+            S[a2] = acc + acc2;
+        }
+    };
+    // Chunk pairs in the loop (the two operand sets stay in fixed registers)
+    // and an odd last chunk after it: no path leaves the loop body midway, so
+    // the compiler's wait placement sees the same outstanding loads on every
+    // iteration and never waits for the next chunk's operands early.
+    int n = 0;
+    for (; n + 1 < a.n_chunks; n += 2) {
+        chunk(n, ops[0], ops[1]);
+        chunk(n + 1, ops[1], ops[0]);
     }
+    if (n < a.n_chunks) chunk(n, ops[0], ops[1]);
 
     // ---- final state (transposed layout: element (i, c) of head h at h*16384 + c*128 + i)
     float* so = a.state_out + (int64_t)b * (a.so_nb3 / 4) + (int64_t)h * 16384;
