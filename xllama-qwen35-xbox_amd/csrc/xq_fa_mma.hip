@@ -81,7 +81,8 @@ struct DecCfg {
     static constexpr int RING = NW * RING_W;
     static constexpr int QIMG = RING;                       // Q image after the K/V rings
     static constexpr int MASKR = QIMG + NPP * QRB;          // mask rings after the Q image
-    static constexpr int MERGE = NW * 16 * D * 4;
+    static constexpr int MS = D + 4;                        // merge row stride (floats)
+    static constexpr int MERGE = NW * 16 * MS * 4;
     static constexpr int LOOP = MASKR + NW * MASK_W;
     static constexpr int SMEM = LOOP > MERGE ? LOOP : MERGE;
     static constexpr bool FITS = SMEM + 2 * NW * NPP * 4 + 64 <= 160 * 1024;
@@ -749,7 +750,10 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // ---- merge the wave states per 16-pair group through LDS (fixed wave order)
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
     __syncthreads();  // every wave is done with its ring and the Q image
-    float* mb = (float*)smem;  // [NW][16][D]
+    // [NW][16][MS]: rows padded by 4 floats so the 16 rows a write instruction
+    // touches start on different banks (unpadded, a 16-way conflict)
+    constexpr int MS = C::MS;
+    float* mb = (float*)smem;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const float lt = xrow_sum(l_run[m]);
@@ -757,13 +761,22 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             sM[wave][16 * m + lr] = m_run[m] == -INFINITY ? -INFINITY : m_run[m] + kPOff;
             sL[wave][16 * m + lr] = lt;
         }
-        float* mw = mb + (wave * 16 + lr) * D;
+        float* mw = mb + (wave * 16 + lr) * MS;
+        // the lane's dims of block c as 16-byte writes (acc_dim's layout);
+        // padding pairs are never read
+        if (16 * m + lr < npa) {
 #pragma unroll
-        for (int c = 0; c < NB; ++c)
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mw[acc_dim<KT>(c, t, lg, i)] = acc[m][2 * c + t][i];
+            for (int c = 0; c < NB; ++c) {
+                const f4 x0 = acc[m][2 * c], x1 = acc[m][2 * c + 1];
+                if constexpr (KT == XQ_TYPE_Q4_0) {
+                    *(f4*)(mw + acc_dim<KT>(c, 0, lg, 0)) = x0;
+                    *(f4*)(mw + acc_dim<KT>(c, 1, lg, 0)) = x1;
+                } else {
+                    *(f4*)(mw + acc_dim<KT>(c, 0, lg, 0)) = f4{x0[0], x1[0], x0[1], x1[1]};
+                    *(f4*)(mw + acc_dim<KT>(c, 0, lg, 2)) = f4{x0[2], x1[2], x0[3], x1[3]};
+                }
+            }
+        }
         __syncthreads();
         for (int e = tid; e < 16 * (D / 4); e += NT) {
             const int pl = e / (D / 4), d4 = e % (D / 4);
@@ -779,7 +792,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 const float mw_ = sM[w][p];
                 const float ew = mw_ == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
                 Ls = fmaf(sL[w][p], ew, Ls);
-                o += ew * *(const f4*)(mb + (w * 16 + pl) * D + 4 * d4);
+                o += ew * *(const f4*)(mb + (w * 16 + pl) * MS + 4 * d4);
             }
             const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
             const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
