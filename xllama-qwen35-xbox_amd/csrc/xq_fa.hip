@@ -749,11 +749,10 @@ size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_spli
 
 hipError_t fa_reduce_launch(const FaArgs& a, int d, hipStream_t stream) {
     const int64_t n_rows = (int64_t)a.B * a.NQ * a.H;
-    ProfScope ps("fa_reduce", stream);
     if (d == 128)
-        hipLaunchKernelGGL(fa_reduce<128>, dim3((uint32_t)n_rows), dim3(128), 0, stream, a);
+        launch("fa_reduce", fa_reduce<128>, dim3((uint32_t)n_rows), dim3(128), stream, a);
     else
-        hipLaunchKernelGGL(fa_reduce<256>, dim3((uint32_t)n_rows), dim3(256), 0, stream, a);
+        launch("fa_reduce", fa_reduce<256>, dim3((uint32_t)n_rows), dim3(256), stream, a);
     return hipGetLastError();
 }
 
@@ -827,11 +826,8 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
             if (L.workspace_bytes < base + fa_mask_pack_bytes(L.mask, a.L, NQ)) return hipErrorInvalidValue;
             uint32_t* packed = (uint32_t*)(ws + base);
             const int n_pack = NQ * a.m_ne2 * a.m_ne3;
-            {
-                ProfScope ps("fa_mask_pack", stream);
-                hipLaunchKernelGGL(fa_mask_pack, dim3((uint32_t)n_pack), dim3(256), 0, stream, a.mask, a.m_nb1,
-                                   a.m_nb2, a.m_nb3, NQ, a.m_ne2, a.L, packed);
-            }
+            launch("fa_mask_pack", fa_mask_pack, dim3((uint32_t)n_pack), dim3(256), stream, a.mask, a.m_nb1,
+                   a.m_nb2, a.m_nb3, NQ, a.m_ne2, a.L, packed);
             a.mask = (const uint8_t*)packed;
             a.m_nb1 = mask_pack_cols(a.L) * 2;
             a.m_nb2 = (int64_t)NQ * a.m_nb1;
@@ -842,16 +838,10 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
     Pass1Fn p1 = pass1_lookup(kt, D, L.qk_mode, np);
     QprepFn qp = D == 128 ? qprep_d<128>(kt, L.qk_mode) : qprep_d<256>(kt, L.qk_mode);
     if (!p1 || !qp) return hipErrorInvalidValue;
-    {
-        ProfScope ps("fa_qprep", stream);
-        hipLaunchKernelGGL(qp, dim3((uint32_t)n_rows), dim3(64), 0, stream, (const uint8_t*)q->data,
-                           (int64_t)q->nb[1], (int64_t)q->nb[2], (int64_t)q->nb[3], NQ, H, L.q_round_f16, qimg);
-    }
+    launch("fa_qprep", qp, dim3((uint32_t)n_rows), dim3(64), stream, (const uint8_t*)q->data,
+           (int64_t)q->nb[1], (int64_t)q->nb[2], (int64_t)q->nb[3], NQ, H, L.q_round_f16, qimg);
     const uint32_t n_wg = (uint32_t)L.n_splits * a.n_qtiles * Hkv * B;
-    {
-        ProfScope ps("fa_pass1", stream);
-        hipLaunchKernelGGL(p1, dim3(n_wg), dim3(kThreads), 0, stream, a, (const uint32_t*)qimg);
-    }
+    launch("fa_pass1", p1, dim3(n_wg), dim3(kThreads), stream, a, (const uint32_t*)qimg);
     if (L.n_splits > 1) return fa_reduce_launch(a, D, stream);
     return hipGetLastError();
 }

@@ -897,10 +897,7 @@ hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
     a.q_nb3 = (int64_t)L.q->nb[3];
     if (!fa_mma_mask_ok(a)) return hipErrorInvalidValue;
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
-    {
-        ProfScope ps("fa_dec", stream);
-        hipLaunchKernelGGL(fn, dim3(n_wg), dim3(64 * waves), 0, stream, a);
-    }
+    launch("fa_dec", fn, dim3(n_wg), dim3(64 * waves), stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.n_splits == 1) return e;
     return fa_reduce_launch(a, D, stream);

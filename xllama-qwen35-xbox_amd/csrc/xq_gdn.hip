@@ -191,9 +191,9 @@ template <bool BF16, bool VEC>
 static void step_dispatch(const GdnStepArgs& a, hipStream_t stream) {
     const dim3 grid(a.B * 32 * (128 / (16 * kStepCpt)));
     if (a.T == 1)
-        hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, kStepCpt, true>), grid, dim3(256), 0, stream, a);
+        launch("gdn_step", gdn_step_kernel<BF16, VEC, kStepCpt, true>, grid, dim3(256), stream, a);
     else
-        hipLaunchKernelGGL((gdn_step_kernel<BF16, VEC, kStepCpt, false>), grid, dim3(256), 0, stream, a);
+        launch("gdn_step", gdn_step_kernel<BF16, VEC, kStepCpt, false>, grid, dim3(256), stream, a);
 }
 
 hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
@@ -223,7 +223,6 @@ hipError_t gdn_step_launch(const GdnLaunch& L, hipStream_t stream) {
         vec = vec && ((uintptr_t)t->data % al == 0);
         for (int i = 1; i < 4; ++i) vec = vec && (t->nb[i] % al == 0);
     }
-    ProfScope ps("gdn_step", stream);
     if (bf16) {
         if (vec) step_dispatch<true, true>(a, stream);
         else step_dispatch<true, false>(a, stream);

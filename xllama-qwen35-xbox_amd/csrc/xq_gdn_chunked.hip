@@ -621,14 +621,8 @@ bool gdn_chunked_available() { return true; }
 
 template <bool BF16, bool VEC>
 static void chunked_kernels(const GdnChunkArgs& a, hipStream_t stream) {
-    {
-        ProfScope ps("gdn_chunk_prep", stream);
-        hipLaunchKernelGGL((gdn_chunk_prep<BF16, VEC>), dim3(a.n_chunks, 32, (uint32_t)a.B), dim3(256), 0, stream, a);
-    }
-    {
-        ProfScope ps("gdn_chunk_scan", stream);
-        hipLaunchKernelGGL((gdn_chunk_scan<BF16, VEC>), dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), 0, stream, a);
-    }
+    launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(a.n_chunks, 32, (uint32_t)a.B), dim3(256), stream, a);
+    launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC>, dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), stream, a);
 }
 
 hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {

@@ -2,6 +2,7 @@
 // and the gfx950 kernels. Shapes arrive here already validated.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -11,20 +12,24 @@
 
 namespace xq {
 
-// Brackets one kernel launch with HIP events while profiling is enabled.
-class ProfScope {
-  public:
-    ProfScope(const char* name, hipStream_t stream);
-    ~ProfScope();
-    ProfScope(const ProfScope&) = delete;
-    ProfScope& operator=(const ProfScope&) = delete;
+// Per-kernel device timing. While profiling is enabled (and the stream is not
+// being captured into a graph), launch() hands the kernel a start/stop HIP
+// event pair that the dispatch itself records at the kernel's first wave and
+// at its completion (hipExtLaunchKernelGGL), so the elapsed time is the
+// kernel's own execution interval, without the host's launch latency.
+bool prof_events(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop);
+void prof_commit(const char* name, hipEvent_t start, hipEvent_t stop);
 
-  private:
-    const char* name_;
-    hipStream_t stream_;
-    hipEvent_t start_{}, stop_{};
-    bool active_ = false;
-};
+template <typename F, typename... Args>
+inline void launch(const char* name, F kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
+    hipEvent_t start, stop;
+    if (prof_events(stream, &start, &stop)) {
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
+        prof_commit(name, start, stop);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+    }
+}
 
 // ---------------------------------------------------------------- storage
 

@@ -127,16 +127,18 @@ hipError_t kv_store_launch(const float* src, const int32_t* positions, int32_t n
                            int32_t q8_variant, void* dst, int32_t capacity, hipStream_t stream) {
     const dim3 grid((uint32_t)n_tokens * (uint32_t)n_head_kv);
     if (grid.x == 0) return hipSuccess;
-    ProfScope ps("kv_store", stream);
     switch (head_dim) {
     case 64:
-        hipLaunchKernelGGL(kv_store_kernel<64>, grid, dim3(64), 0, stream, src, positions, n_head_kv, kv_type, q8_variant, (uint8_t*)dst, capacity);
+        launch("kv_store", kv_store_kernel<64>, grid, dim3(64), stream, src, positions, n_head_kv, kv_type, q8_variant,
+               (uint8_t*)dst, capacity);
         break;
     case 128:
-        hipLaunchKernelGGL(kv_store_kernel<128>, grid, dim3(64), 0, stream, src, positions, n_head_kv, kv_type, q8_variant, (uint8_t*)dst, capacity);
+        launch("kv_store", kv_store_kernel<128>, grid, dim3(64), stream, src, positions, n_head_kv, kv_type, q8_variant,
+               (uint8_t*)dst, capacity);
         break;
     case 256:
-        hipLaunchKernelGGL(kv_store_kernel<256>, grid, dim3(64), 0, stream, src, positions, n_head_kv, kv_type, q8_variant, (uint8_t*)dst, capacity);
+        launch("kv_store", kv_store_kernel<256>, grid, dim3(64), stream, src, positions, n_head_kv, kv_type, q8_variant,
+               (uint8_t*)dst, capacity);
         break;
     default:
         return hipErrorInvalidValue;

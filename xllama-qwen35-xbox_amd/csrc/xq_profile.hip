@@ -26,22 +26,21 @@ std::vector<Pending> g_pending;
 std::map<std::string, Total> g_totals;
 }  // namespace
 
-ProfScope::ProfScope(const char* name, hipStream_t stream) : name_(name), stream_(stream) {
-    if (!g_on.load(std::memory_order_relaxed)) return;
-    if (hipEventCreate(&start_) != hipSuccess) return;
-    if (hipEventCreate(&stop_) != hipSuccess) {
-        (void)hipEventDestroy(start_);
-        return;
+bool prof_events(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop) {
+    if (!g_on.load(std::memory_order_relaxed)) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+    if (hipEventCreate(start) != hipSuccess) return false;
+    if (hipEventCreate(stop) != hipSuccess) {
+        (void)hipEventDestroy(*start);
+        return false;
     }
-    (void)hipEventRecord(start_, stream_);
-    active_ = true;
+    return true;
 }
 
-ProfScope::~ProfScope() {
-    if (!active_) return;
-    (void)hipEventRecord(stop_, stream_);
+void prof_commit(const char* name, hipEvent_t start, hipEvent_t stop) {
     std::lock_guard<std::mutex> lk(g_mu);
-    g_pending.push_back({name_, start_, stop_});
+    g_pending.push_back({name, start, stop});
 }
 
 }  // namespace xq
