@@ -132,7 +132,7 @@ XQ_DEV f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f
 // ---------------------------------------------------------------- prep
 
 template <bool BF16, bool VEC>
-__global__ __launch_bounds__(256, 2) void gdn_chunk_prep(GdnChunkArgs a) {
+__global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs a) {
     constexpr int KP = 136;  // padded f16 row stride (halves)
     constexpr int TP = 72;   // K^T row stride (halves)
     constexpr int FP = 65;   // padded f32 row stride
