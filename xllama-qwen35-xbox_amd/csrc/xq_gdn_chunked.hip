@@ -135,13 +135,13 @@ template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs a) {
     constexpr int KP = 136;  // padded f16 row stride (halves)
     constexpr int TP = 72;   // K^T row stride (halves)
-    constexpr int FP = 65;   // padded f32 row stride
+    constexpr int FP = 68;   // padded f32 row stride (16-byte rows, conflict-free MFMA stores)
     // 68.6 KB for bf16 rows: two workgroups per CU. sKT holds K^T for the record; after the
     // products sK becomes T and sQ the P planes.
     __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][65]
     __shared__ __attribute__((aligned(16))) _Float16 sKT[128 * TP];  // K^T [i][t]
     __shared__ __attribute__((aligned(16))) _Float16 sQ[64 * KP];    // Q [t][i], then P hi, lo [64][64]
-    __shared__ float sKK[64 * FP];  // K K^T, then L
+    __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // K K^T, then L
     __shared__ float sG[64], sBeta[64], sEG[64];
     // f32 rows: the f16 remainders of K, K^T and Q (+52 KB: one workgroup per CU)
     constexpr int NKL = BF16 ? 8 : 64 * KP, NKTL = BF16 ? 8 : 128 * TP;
@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         }
     }
     // ---- L (strictly lower, in place of K K^T)
+#pragma unroll 4
     for (int e = tid; e < 64 * 64; e += 256) {
         const int t = e >> 6, j = e & 63;
         const float L = j < t ? sBeta[t] * __expf(sEG[t] - sEG[j]) * sKK[t * FP + j] : 0.0f;
@@ -253,7 +254,10 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     __syncthreads();
     // ---- T = (I + L)^{-1} diag(beta): column j by a quad of lanes; lane part p
     //      keeps x_s for s in [16p, 16p + 16) and the quad sums the dot products
-    //      (four partial chains per lane)
+    //      (four partial chains per lane). Row t of L (the lane's 16 values,
+    //      four 16-byte reads) is loaded two steps ahead: the loop is a chain of
+    //      64 dependent steps, and a read issued in its own step would put the
+    //      LDS latency into every one of them.
     float* sT = (float*)sK;  // T [t][j], f32
     {
         const int j = wave * 16 + (lane >> 2), p = lane & 3;
@@ -261,14 +265,23 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
 #pragma unroll
         for (int m = 0; m < 16; ++m) x[m] = 0.0f;
         const float bj = sBeta[j];
+        f4 Lq[3][4];  // rows t, t + 1, t + 2 (ring by t % 3)
+        auto ldrow = [&](int t, f4 (&r)[4]) {
+            const f4* Lr = (const f4*)(sKK + t * FP + 16 * p);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) r[u] = Lr[u];
+        };
+        ldrow(1, Lq[1]);
+        ldrow(2, Lq[2]);
 #pragma unroll
         for (int t = 0; t < 64; ++t) {
             float part = 0.0f;
             if (t > 0) {
-                const float* Lr = sKK + t * FP + 16 * p;
+                if (t + 2 < 64) ldrow(t + 2, Lq[(t + 2) % 3]);
+                const f4 (&Lr)[4] = Lq[t % 3];
                 float c4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int m = 0; m < 16; ++m) c4[m & 3] = fmaf(Lr[m], x[m], c4[m & 3]);  // L[t][s >= t] = 0
+                for (int m = 0; m < 16; ++m) c4[m & 3] = fmaf(Lr[m >> 2][m & 3], x[m], c4[m & 3]);  // L[t][s >= t] = 0
                 part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
             }
             part += dpp<0xB1>(part);  // quad: lanes p ^ 1
