@@ -17,24 +17,28 @@
 //
 // Two kernels:
 //   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
-//                   parallel: K K^T and Q K^T on f16 MFMA (f32 accumulation),
-//                   the unit lower-triangular solve for T in f32, P with its
-//                   decays; stores T and P as f16 hi + lo planes, K^T as f16
-//                   and the decay vectors (49 KB per chunk) in the workspace.
-//                   f32 q / k rows enter as f16 hi + lo (the products take
-//                   hi*hi + hi*lo + lo*hi) and the record also keeps K^T lo
-//                   (65 KB); bf16 rows are f16 values already (their 8
-//                   significant bits fit, down to 2^-24).
+//                   parallel: K K^T on f16 MFMA (f32 accumulation) and the unit
+//                   lower-triangular solve for T in f32; stores T as f16 hi + lo
+//                   planes, K^T as f16, the decay vectors and the cumulative
+//                   log-decays G (33 KB per chunk) in the workspace. f32 k rows
+//                   enter as f16 hi + lo (the products take hi*hi + hi*lo +
+//                   lo*hi) and the record also keeps K^T lo (49 KB); bf16 rows
+//                   are f16 values already (their 8 significant bits fit, down
+//                   to 2^-24).
 //   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
 //                   the chunks in order with its 128 x 16 state block in
 //                   registers (f32). Every MFMA operand that does not depend on
 //                   the state (K and Q rows straight from the inputs, as f16,
-//                   or f16 hi + lo for f32 rows; K^T, T and P rows from the workspace;
-//                   V and the decays) is loaded into registers a chunk ahead;
-//                   LDS carries only the state-dependent exchanges (S^T, X^T,
-//                   U^T). The products run on v_mfma_f32_16x16x32_f16 with f32
-//                   operands split into f16 hi + lo (about 22 significant bits),
-//                   so the result stays within f32-recurrence tolerances.
+//                   or f16 hi + lo for f32 rows; K^T and T rows from the
+//                   workspace; V, the decays and G) is loaded into registers a
+//                   chunk ahead. P is formed in the scan from the K and Q rows
+//                   it already holds (the waves share their K rows through
+//                   LDS), which keeps 16 KB per chunk out of every workgroup's
+//                   operand fetch, the scan's limit. LDS otherwise carries the
+//                   state-dependent exchanges (S^T, X^T, U^T). The products run
+//                   on f16 MFMA with f32 operands split into f16 hi + lo (about
+//                   22 significant bits), so the result stays within
+//                   f32-recurrence tolerances.
 // The 8 column blocks of a head run on one XCD (consecutive logical workgroups)
 // so the chunk rows and T, P they share are read from HBM once.
 #include <type_traits>
@@ -54,10 +58,9 @@ constexpr int kColBlocks = 128 / kCols;
 // Workspace record of one (sequence, v-head, chunk), byte offsets.
 constexpr int kRecTHi = 0;                       // f16 [64][64]
 constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
-constexpr int kRecPHi = kRecTLo + 64 * 64 * 2;  // f16 [64][64]
-constexpr int kRecPLo = kRecPHi + 64 * 64 * 2;
-constexpr int kRecKT = kRecPLo + 64 * 64 * 2;  // f16 K^T [128][64]
-constexpr int kRecDec = kRecKT + 128 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}
+constexpr int kRecKT = kRecTLo + 64 * 64 * 2;   // f16 K^T [128][64]
+constexpr int kRecDec = kRecKT + 128 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, G[64] at 192
+constexpr int kRecG = 192;                      // G offset in floats within the decays
 constexpr int kRecKTLo = kRecDec + 1024;        // f32 rows only: f16 K^T lo [128][64]
 template <bool BF16>
 constexpr int rec_bytes() { return BF16 ? kRecKTLo : kRecKTLo + 128 * 64 * 2; }
@@ -128,6 +131,7 @@ XQ_DEV h8 lo_h8(const float (&x)[8], h8 hi) {
 }
 
 XQ_DEV f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+XQ_DEV f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
 // ---------------------------------------------------------------- prep
 
@@ -136,17 +140,16 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     constexpr int KP = 136;  // padded f16 row stride (halves)
     constexpr int TP = 72;   // K^T row stride (halves)
     constexpr int FP = 68;   // padded f32 row stride (16-byte rows, conflict-free MFMA stores)
-    // 68.6 KB for bf16 rows: two workgroups per CU. sKT holds K^T for the record; after the
-    // products sK becomes T and sQ the P planes.
-    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][65]
+    // 53 KB for bf16 rows: two workgroups per CU. sKT holds K^T for the record;
+    // after the products sK becomes T.
+    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][FP]
     __shared__ __attribute__((aligned(16))) _Float16 sKT[128 * TP];  // K^T [i][t]
-    __shared__ __attribute__((aligned(16))) _Float16 sQ[64 * KP];    // Q [t][i], then P hi, lo [64][64]
     __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // K K^T, then L
     __shared__ float sG[64], sBeta[64], sEG[64];
-    // f32 rows: the f16 remainders of K, K^T and Q (+52 KB: one workgroup per CU)
+    // f32 rows: the f16 remainders of K and K^T (+35 KB: one workgroup per CU)
     constexpr int NKL = BF16 ? 8 : 64 * KP, NKTL = BF16 ? 8 : 128 * TP;
-    __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL], sKTl[NKTL], sQl[NKL];
-    static_assert(64 * FP * 4 <= 64 * KP * 2 && 2 * 64 * 64 * 2 <= 64 * KP * 2, "LDS aliases");
+    __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL], sKTl[NKTL];
+    static_assert(64 * FP * 4 <= 64 * KP * 2, "LDS aliases");
 
     const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int kh = h % 16;
@@ -161,27 +164,23 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         const int tg = t0 + t;
         const bool ok = tg < a.T;
         const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tg * a.k_nb2 + (int64_t)kh * a.k_nb1;
-        const uint8_t* qr = a.q + (int64_t)b * a.q_nb3 + (int64_t)tg * a.q_nb2 + (int64_t)kh * a.q_nb1;
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
             const int i0 = 32 * qt + 8 * gi;
-            float xk[8], xq[8];
+            float xk[8];
             if (ok) {
                 load8<BF16, VEC>(kr, i0, xk);
-                load8<BF16, VEC>(qr, i0, xq);
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xk[e] = xq[e] = 0.0f;
+                for (int e = 0; e < 8; ++e) xk[e] = 0.0f;
             }
-            const h8 hk = to_h8(xk), hq = to_h8(xq);
+            const h8 hk = to_h8(xk);
             *(h8*)(sK + t * KP + i0) = hk;
-            *(h8*)(sQ + t * KP + i0) = hq;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sKT[(i0 + e) * TP + t] = hk[e];
             if constexpr (!BF16) {
                 const h8 lk = lo_h8(xk, hk);
                 *(h8*)(sKl + t * KP + i0) = lk;
-                *(h8*)(sQl + t * KP + i0) = lo_h8(xq, hq);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) sKTl[(i0 + e) * TP + t] = lk[e];
             }
@@ -200,50 +199,28 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         for (int s = 0; s <= tid; ++s) G += sG[s];
         sEG[tid] = G;
     }
-    // ---- K K^T and Q K^T: 16 tiles each, 4 per wave, contraction over 128 key dims
-    f4 qk[4];
+    // ---- K K^T: 16 tiles, 4 per wave, contraction over 128 key dims
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
         const int tile = wave * 4 + tt;
         const int mt = tile >> 2, nt = tile & 3;
         f4 kk = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        qk[tt] = kk;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 bk = *(const h8*)(sK + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
             const h8 ak = *(const h8*)(sK + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
-            const h8 aq = *(const h8*)(sQ + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
             kk = mfma32(ak, bk, kk);
-            qk[tt] = mfma32(aq, bk, qk[tt]);
             if constexpr (!BF16) {
                 const h8 bkl = *(const h8*)(sKl + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
                 const h8 akl = *(const h8*)(sKl + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
-                const h8 aql = *(const h8*)(sQl + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
                 kk = mfma32(ak, bkl, kk);
                 kk = mfma32(akl, bk, kk);
-                qk[tt] = mfma32(aq, bkl, qk[tt]);
-                qk[tt] = mfma32(aql, bk, qk[tt]);
             }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) sKK[(mt * 16 + 4 * lg + r) * FP + nt * 16 + lr] = kk[r];
     }
-    __syncthreads();  // K, Q no longer read; G ready
-    // ---- P = (Q K^T) e^{G_t - G_j} (j <= t) as f16 hi, lo planes in place of Q
-    _Float16* sPh = sQ;
-    _Float16* sPl = sQ + 64 * 64;
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-        const int tile = wave * 4 + tt;
-        const int mt = tile >> 2, nt = tile & 3;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = mt * 16 + 4 * lg + r, j = nt * 16 + lr;
-            const float pv = j <= t ? qk[tt][r] * __expf(sEG[t] - sEG[j]) : 0.0f;
-            sPh[t * 64 + j] = f16_hi(pv);
-            sPl[t * 64 + j] = f16_lo(pv);
-        }
-    }
+    __syncthreads();  // K no longer read; G ready
     // ---- L (strictly lower, in place of K K^T)
 #pragma unroll 4
     for (int e = tid; e < 64 * 64; e += 256) {
@@ -294,8 +271,8 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     }
     __syncthreads();
 
-    // ---- the record: T (f16 hi + lo), P (hi, lo), K^T (f16) with 16-byte
-    //      stores, and the decays
+    // ---- the record: T (f16 hi + lo), K^T (f16) with 16-byte stores, the
+    //      decays and G
     uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
     {
         const int t = tid >> 2, j0 = 16 * (tid & 3);
@@ -310,8 +287,6 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         for (int u = 0; u < 2; ++u) {
             *(h8*)(rec + kRecTHi + o + 16 * u) = th[u];
             *(h8*)(rec + kRecTLo + o + 16 * u) = tl[u];
-            *(h8*)(rec + kRecPHi + o + 16 * u) = *(const h8*)(sPh + t * 64 + j0 + 8 * u);
-            *(h8*)(rec + kRecPLo + o + 16 * u) = *(const h8*)(sPl + t * 64 + j0 + 8 * u);
         }
     }
 #pragma unroll
@@ -327,6 +302,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         float* dec = (float*)(rec + kRecDec);
         dec[tid] = __expf(G);
         dec[64 + tid] = __expf(GC - G);
+        dec[kRecG + tid] = G;
         if (tid == 0) dec[128] = __expf(GC);
     }
 }
@@ -335,23 +311,25 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
 
 // Operands of one chunk for one wave of a scan workgroup, loaded a chunk ahead:
 // A operands (row 16w + lr of the wave's token tile, k = 32 ks + 8 lg .. +7) of
-// K and Q (raw input words, decoded when used), of T and P (hi, lo), and of
-// K^T for the wave's key-dim tiles 2w, 2w + 1; the raw V values and e^G,
-// e^{G_C - G} of the lane's four tokens 16w + 4lg + r (column 16cb + lr), and
-// e^{G_C}. Every load is unconditional (token and chunk indices are clamped
+// K and Q (raw input words, decoded when used), of T (hi, lo), and of K^T for
+// the wave's key-dim tiles 2w, 2w + 1; the raw V values and e^G, e^{G_C - G}
+// of the lane's four tokens 16w + 4lg + r (column 16cb + lr), e^{G_C}, and the
+// G values P needs (token 16w + lr, tokens 16jt + 4lg + i). Every load is unconditional (token and chunk indices are clamped
 // into range and out-of-range tokens masked at use), so the compiler's waits
 // for a chunk's operands never include the next chunk's loads.
 template <bool BF16, bool VEC>
 struct ScanOps {
     static constexpr int KW = VEC ? (BF16 ? 1 : 2) : 4;  // 16-byte words per 8 elements (VEC), else raw dwords
     uint4 kw[4][KW], qw[4][KW];
-    h8 th[2], tl[2], ph[2], pl[2], kt[2][2];
+    h8 th[2], tl[2], kt[2][2];
     h8 ktl[BF16 ? 1 : 2][2];  // K^T lo (f32 rows)
     // raw V words, in the input's width: a 16-bit load widened at use (widened
     // here, the compiler copies the value at the loop edge and waits for it)
     std::conditional_t<BF16, uint16_t, uint32_t> vw[4];
     float4 eg, egc;
     float eGC;
+    float gt;       // G of token 16w + lr
+    f4 gj[4];       // G of tokens 16jt + 4lg + i
     bool ok;        // the A-operand token is in range
     uint32_t vok;   // bit r: token 16w + 4lg + r is in range
 };
@@ -408,12 +386,18 @@ XQ_DEV h8 decode8(const uint4 (&w)[KW], bool ok) {
     return r;
 }
 
-template <bool BF16, bool VEC>
+// The operands of chunk n in four parts, each issued in its own phase of the
+// previous chunk's step (between its barriers), in the order the step uses
+// them: a burst of all of them at the start of a step stalls the wave while
+// the loads queue. Part 0: K and Q rows; 1: T; 2: K^T, the decays and G;
+// 3: V.
+template <int PART, bool BF16, bool VEC>
 XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wave, int lr, int lg,
                       ScanOps<BF16, VEC>& L) {
     const int kh = h % 16;
     n = min(n, a.n_chunks - 1);  // the prefetch past the last chunk re-reads it
-    {
+    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
+    if constexpr (PART == 0) {
         const int tg = n * kChunk + 16 * wave + lr;  // A-operand row token
         L.ok = tg < a.T;
         const int tc = min(tg, a.T - 1);
@@ -424,39 +408,54 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
             load_raw8<BF16, VEC>(kr, 32 * ks + 8 * lg, L.kw[ks]);
             load_raw8<BF16, VEC>(qr, 32 * ks + 8 * lg, L.qw[ks]);
         }
-    }
-    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
+    } else if constexpr (PART == 1) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int o = ((16 * wave + lr) * 64 + 32 * ks + 8 * lg) * 2;
-        L.th[ks] = *(const h8*)(rec + kRecTHi + o);
-        L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
-        L.ph[ks] = *(const h8*)(rec + kRecPHi + o);
-        L.pl[ks] = *(const h8*)(rec + kRecPLo + o);
+        for (int ks = 0; ks < 2; ++ks) {
+            const int o = ((16 * wave + lr) * 64 + 32 * ks + 8 * lg) * 2;
+            L.th[ks] = *(const h8*)(rec + kRecTHi + o);
+            L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
+        }
+    } else if constexpr (PART == 2) {
 #pragma unroll
-        for (int a2 = 0; a2 < 2; ++a2) {
-            const int ko = ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2;
-            L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ko);
-            if constexpr (!BF16) L.ktl[a2][ks] = *(const h8*)(rec + kRecKTLo + ko);
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+            for (int a2 = 0; a2 < 2; ++a2) {
+                const int ko = ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2;
+                L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ko);
+                if constexpr (!BF16) L.ktl[a2][ks] = *(const h8*)(rec + kRecKTLo + ko);
+            }
+        }
+        const float* dec = (const float*)(rec + kRecDec);
+        L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
+        L.egc = *(const float4*)(dec + 64 + 16 * wave + 4 * lg);
+        L.eGC = dec[128];
+        L.gt = dec[kRecG + 16 * wave + lr];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + kRecG + 16 * jt + 4 * lg);
+    } else {
+        L.vok = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tg = n * kChunk + 16 * wave + 4 * lg + r;
+            L.vok |= (tg < a.T ? 1u : 0u) << r;
+            const int tc = min(tg, a.T - 1);
+            const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tc * a.v_nb2 + (int64_t)h * a.v_nb1;
+            const int c = kCols * cb + lr;
+            if constexpr (BF16)
+                L.vw[r] = ((const uint16_t*)vr)[c];
+            else
+                L.vw[r] = ((const uint32_t*)vr)[c];
         }
     }
-    const float* dec = (const float*)(rec + kRecDec);
-    L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
-    L.egc = *(const float4*)(dec + 64 + 16 * wave + 4 * lg);
-    L.eGC = dec[128];
-    L.vok = 0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int tg = n * kChunk + 16 * wave + 4 * lg + r;
-        L.vok |= (tg < a.T ? 1u : 0u) << r;
-        const int tc = min(tg, a.T - 1);
-        const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tc * a.v_nb2 + (int64_t)h * a.v_nb1;
-        const int c = kCols * cb + lr;
-        if constexpr (BF16)
-            L.vw[r] = ((const uint16_t*)vr)[c];
-        else
-            L.vw[r] = ((const uint32_t*)vr)[c];
-    }
+}
+
+template <bool BF16, bool VEC>
+XQ_DEV void scan_load_all(const GdnChunkArgs& a, int b, int h, int cb, int n, int wave, int lr, int lg,
+                          ScanOps<BF16, VEC>& L) {
+    scan_load<0>(a, b, h, cb, n, wave, lr, lg, L);
+    scan_load<1>(a, b, h, cb, n, wave, lr, lg, L);
+    scan_load<2>(a, b, h, cb, n, wave, lr, lg, L);
+    scan_load<3>(a, b, h, cb, n, wave, lr, lg, L);
 }
 
 template <bool BF16, bool VEC>
@@ -467,6 +466,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sXh[kCols * TP], sXl[kCols * TP];  // X^T
     __shared__ __attribute__((aligned(16))) _Float16 sUh[kCols * TP], sUl[kCols * TP];  // U^T
     __shared__ __attribute__((aligned(16))) _Float16 sWh[kCols * TP], sWl[kCols * TP];  // (e^{G_C - G} U)^T
+    // K rows of the chunk [t][i] (f16 hi, and lo for f32 rows): the A operands of P^T = K Q^T
+    __shared__ __attribute__((aligned(16))) _Float16 sKh[64 * SP], sKl[BF16 ? 8 : 64 * SP];
 
     const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
     const uint32_t wg = xcd_remap(blockIdx.x, n_wg);  // column blocks of a head adjacent (one XCD)
@@ -488,11 +489,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
 
     ScanOps<BF16, VEC> ops[2];
-    scan_load<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
+    scan_load_all<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
     // One chunk: C holds its operands (loaded a chunk ahead), the next chunk's
-    // operands are loaded into Nx.
+    // operands are loaded into Nx part by part.
     auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx) {
-        scan_load<BF16, VEC>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
+        scan_load<0>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
+
+        // ---- the wave's K rows -> LDS (every wave forms its P from all of them)
+        h8 ak[4], aq[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            ak[ks] = decode8<BF16, VEC>(C.kw[ks], C.ok);
+            aq[ks] = decode8<BF16, VEC>(C.qw[ks], C.ok);
+            const int ko = (16 * wave + lr) * SP + 32 * ks + 8 * lg;
+            *(h8*)(sKh + ko) = ak[ks];
+            if constexpr (!BF16) *(h8*)(sKl + ko) = decode8_lo(C.kw[ks], C.ok);
+        }
 
         // ---- S (hi, lo) -> LDS as S^T [c][i]: the B operand rows of K S and Q S
 #pragma unroll
@@ -505,18 +517,18 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
             *(h4*)(sSl + lr * SP + 16 * it + 4 * lg) = sl;
         }
         __syncthreads();
+        scan_load<1>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
 
         // ---- K S and Q S for token tile w (16 tokens x 16 columns)
         f4 ksh = f4{0.0f, 0.0f, 0.0f, 0.0f}, ksl = ksh, qsh = ksh, qsl = ksh;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            const h8 ak = decode8<BF16, VEC>(C.kw[ks], C.ok), aq = decode8<BF16, VEC>(C.qw[ks], C.ok);
             const int bo = lr * SP + 32 * ks + 8 * lg;
             const h8 bh = *(const h8*)(sSh + bo), bl = *(const h8*)(sSl + bo);
-            ksh = mfma32(ak, bh, ksh);
-            ksl = mfma32(ak, bl, ksl);
-            qsh = mfma32(aq, bh, qsh);
-            qsl = mfma32(aq, bl, qsl);
+            ksh = mfma32(ak[ks], bh, ksh);
+            ksl = mfma32(ak[ks], bl, ksl);
+            qsh = mfma32(aq[ks], bh, qsh);
+            qsl = mfma32(aq[ks], bl, qsl);
             if constexpr (!BF16) {
                 ksl = mfma32(decode8_lo(C.kw[ks], C.ok), bh, ksl);
                 qsl = mfma32(decode8_lo(C.qw[ks], C.ok), bh, qsl);
@@ -536,7 +548,37 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         }
         *(h4*)(sXh + lr * TP + 16 * wave + 4 * lg) = xh;
         *(h4*)(sXl + lr * TP + 16 * wave + 4 * lg) = xl;
+
+        // ---- P[t][j] = (q_t . k_j) e^{G_t - G_j} (j <= t) for t in the wave's
+        //      tile, as P^T = K Q^T per token tile jt <= w: lane (lr, lg) gets
+        //      t = 16w + lr, j = 16jt + 4lg + i, which is the A operand layout of
+        //      the 16x16x16 product Y += P U below
+        h4 ph[4], pl[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            ph[jt] = h4{0, 0, 0, 0};
+            pl[jt] = ph[jt];
+            if (jt > wave) continue;  // wave-uniform
+            f4 pt = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const int ko = (16 * jt + lr) * SP + 32 * ks + 8 * lg;
+                const h8 kj = *(const h8*)(sKh + ko);
+                pt = mfma32(kj, aq[ks], pt);
+                if constexpr (!BF16) {
+                    pt = mfma32(kj, decode8_lo(C.qw[ks], C.ok), pt);
+                    pt = mfma32(*(const h8*)(sKl + ko), aq[ks], pt);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool causal = jt < wave || 4 * lg + i <= lr;
+                const float pv = causal ? pt[i] * __expf(C.gt - C.gj[jt][i]) : 0.0f;
+                ph[jt][i] = f16_hi(pv), pl[jt][i] = f16_lo(pv);
+            }
+        }
         __syncthreads();
+        scan_load<2>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
 
         // ---- U = T X for token tile w; U and e^{G_C - G} U -> LDS as [c][t]
         f4 u = f4{0.0f, 0.0f, 0.0f, 0.0f}, u2 = u;
@@ -565,16 +607,18 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
             *(h4*)(sWl + o) = wl;
         }
         __syncthreads();
+        scan_load<3>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
 
-        // ---- Y = scale (e^G Q S + P U) for token tile w
+        // ---- Y = scale (e^G Q S + P U) for token tile w (P is zero past tile w)
         f4 y = QS, y2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int bo = lr * TP + 32 * ks + 8 * lg;
-            const h8 bh = *(const h8*)(sUh + bo), bl = *(const h8*)(sUl + bo);
-            y = mfma32(C.ph[ks], bh, y);
-            y2 = mfma32(C.ph[ks], bl, y2);
-            y2 = mfma32(C.pl[ks], bh, y2);
+        for (int jt = 0; jt < 4; ++jt) {
+            if (jt > wave) continue;  // wave-uniform
+            const int bo = lr * TP + 16 * jt + 4 * lg;
+            const h4 bh = *(const h4*)(sUh + bo), bl = *(const h4*)(sUl + bo);
+            y = mfma16(ph[jt], bh, y);
+            y2 = mfma16(ph[jt], bl, y2);
+            y2 = mfma16(pl[jt], bh, y2);
         }
         y += y2;
 #pragma unroll
