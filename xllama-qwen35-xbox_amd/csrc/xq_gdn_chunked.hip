@@ -19,23 +19,23 @@
 //   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
 //                   parallel: K K^T on f16 MFMA (f32 accumulation) and the unit
 //                   lower-triangular solve for T in f32; stores T as f16 hi + lo
-//                   planes, K^T as f16, the decay vectors and the cumulative
-//                   log-decays G (33 KB per chunk) in the workspace. f32 k rows
-//                   enter as f16 hi + lo (the products take hi*hi + hi*lo +
-//                   lo*hi) and the record also keeps K^T lo (49 KB); bf16 rows
-//                   are f16 values already (their 8 significant bits fit, down
-//                   to 2^-24).
+//                   planes, the decay vectors and the cumulative log-decays G
+//                   (17 KB per chunk) in the workspace. f32 k rows enter as f16
+//                   hi + lo (the products take hi*hi + hi*lo + lo*hi); bf16
+//                   rows are f16 values already (their 8 significant bits fit,
+//                   down to 2^-24).
 //   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
 //                   the chunks in order with its 128 x 16 state block in
 //                   registers (f32). Every MFMA operand that does not depend on
 //                   the state (K and Q rows straight from the inputs, as f16,
-//                   or f16 hi + lo for f32 rows; K^T and T rows from the
-//                   workspace; V, the decays and G) is loaded into registers a
-//                   chunk ahead. P is formed in the scan from the K and Q rows
-//                   it already holds (the waves share their K rows through
-//                   LDS), which keeps 16 KB per chunk out of every workgroup's
-//                   operand fetch, the scan's limit. LDS otherwise carries the
-//                   state-dependent exchanges (S^T, X^T, U^T). The products run
+//                   or f16 hi + lo for f32 rows; T rows from the workspace; V,
+//                   the decays and G) is loaded into registers a chunk ahead,
+//                   in four parts spread over the chunk's phases. P and K^T are
+//                   formed in the scan from the K and Q rows it already holds
+//                   (the waves share their K rows through LDS, as rows and
+//                   transposed), which keeps 32 KB per chunk out of every
+//                   workgroup's operand fetch, the scan's limit. LDS otherwise
+//                   carries the state-dependent exchanges (S^T, X^T, U^T). The products run
 //                   on f16 MFMA with f32 operands split into f16 hi + lo (about
 //                   22 significant bits), so the result stays within
 //                   f32-recurrence tolerances.
@@ -58,12 +58,9 @@ constexpr int kColBlocks = 128 / kCols;
 // Workspace record of one (sequence, v-head, chunk), byte offsets.
 constexpr int kRecTHi = 0;                       // f16 [64][64]
 constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
-constexpr int kRecKT = kRecTLo + 64 * 64 * 2;   // f16 K^T [128][64]
-constexpr int kRecDec = kRecKT + 128 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, G[64] at 192
+constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, G[64] at 192
 constexpr int kRecG = 192;                      // G offset in floats within the decays
-constexpr int kRecKTLo = kRecDec + 1024;        // f32 rows only: f16 K^T lo [128][64]
-template <bool BF16>
-constexpr int rec_bytes() { return BF16 ? kRecKTLo : kRecKTLo + 128 * 64 * 2; }
+constexpr int kRecBytes = kRecDec + 1024;
 
 struct GdnChunkArgs {
     const uint8_t* q;
@@ -138,17 +135,14 @@ XQ_DEV f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f1
 template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs a) {
     constexpr int KP = 136;  // padded f16 row stride (halves)
-    constexpr int TP = 72;   // K^T row stride (halves)
     constexpr int FP = 68;   // padded f32 row stride (16-byte rows, conflict-free MFMA stores)
-    // 53 KB for bf16 rows: two workgroups per CU. sKT holds K^T for the record;
-    // after the products sK becomes T.
+    // 35 KB for bf16 rows (52 KB for f32 rows); after the products sK becomes T.
     __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][FP]
-    __shared__ __attribute__((aligned(16))) _Float16 sKT[128 * TP];  // K^T [i][t]
     __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // K K^T, then L
     __shared__ float sG[64], sBeta[64], sEG[64];
-    // f32 rows: the f16 remainders of K and K^T (+35 KB: one workgroup per CU)
-    constexpr int NKL = BF16 ? 8 : 64 * KP, NKTL = BF16 ? 8 : 128 * TP;
-    __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL], sKTl[NKTL];
+    // f32 rows: the f16 remainders of K
+    constexpr int NKL = BF16 ? 8 : 64 * KP;
+    __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
     static_assert(64 * FP * 4 <= 64 * KP * 2, "LDS aliases");
 
     const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -176,14 +170,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             }
             const h8 hk = to_h8(xk);
             *(h8*)(sK + t * KP + i0) = hk;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sKT[(i0 + e) * TP + t] = hk[e];
-            if constexpr (!BF16) {
-                const h8 lk = lo_h8(xk, hk);
-                *(h8*)(sKl + t * KP + i0) = lk;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) sKTl[(i0 + e) * TP + t] = lk[e];
-            }
+            if constexpr (!BF16) *(h8*)(sKl + t * KP + i0) = lo_h8(xk, hk);
         }
         if (tid < 64) {
             const int tt = t0 + tid;
@@ -271,9 +258,8 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     }
     __syncthreads();
 
-    // ---- the record: T (f16 hi + lo), K^T (f16) with 16-byte stores, the
-    //      decays and G
-    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
+    // ---- the record: T (f16 hi + lo) with 16-byte stores, the decays and G
+    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
     {
         const int t = tid >> 2, j0 = 16 * (tid & 3);
         h8 th[2], tl[2];
@@ -288,13 +274,6 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             *(h8*)(rec + kRecTHi + o + 16 * u) = th[u];
             *(h8*)(rec + kRecTLo + o + 16 * u) = tl[u];
         }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {  // K^T: 1024 chunks of 8 tokens
-        const int e = tid + 256 * u, i = e >> 3, c8 = e & 7;
-        *(h8*)(rec + kRecKT + (i * 64 + 8 * c8) * 2) = *(const h8*)(sKT + i * TP + 8 * c8);
-        if constexpr (!BF16)
-            *(h8*)(rec + kRecKTLo + (i * 64 + 8 * c8) * 2) = *(const h8*)(sKTl + i * TP + 8 * c8);
     }
     if (tid < 64) {
         const float GC = sEG[63];
@@ -311,8 +290,8 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
 
 // Operands of one chunk for one wave of a scan workgroup, loaded a chunk ahead:
 // A operands (row 16w + lr of the wave's token tile, k = 32 ks + 8 lg .. +7) of
-// K and Q (raw input words, decoded when used), of T (hi, lo), and of K^T for
-// the wave's key-dim tiles 2w, 2w + 1; the raw V values and e^G, e^{G_C - G}
+// K and Q (raw input words, decoded when used) and of T (hi, lo); the raw V
+// values and e^G, e^{G_C - G}
 // of the lane's four tokens 16w + 4lg + r (column 16cb + lr), e^{G_C}, and the
 // G values P needs (token 16w + lr, tokens 16jt + 4lg + i). Every load is unconditional (token and chunk indices are clamped
 // into range and out-of-range tokens masked at use), so the compiler's waits
@@ -321,8 +300,7 @@ template <bool BF16, bool VEC>
 struct ScanOps {
     static constexpr int KW = VEC ? (BF16 ? 1 : 2) : 4;  // 16-byte words per 8 elements (VEC), else raw dwords
     uint4 kw[4][KW], qw[4][KW];
-    h8 th[2], tl[2], kt[2][2];
-    h8 ktl[BF16 ? 1 : 2][2];  // K^T lo (f32 rows)
+    h8 th[2], tl[2];
     // raw V words, in the input's width: a 16-bit load widened at use (widened
     // here, the compiler copies the value at the loop edge and waits for it)
     std::conditional_t<BF16, uint16_t, uint32_t> vw[4];
@@ -389,14 +367,13 @@ XQ_DEV h8 decode8(const uint4 (&w)[KW], bool ok) {
 // The operands of chunk n in four parts, each issued in its own phase of the
 // previous chunk's step (between its barriers), in the order the step uses
 // them: a burst of all of them at the start of a step stalls the wave while
-// the loads queue. Part 0: K and Q rows; 1: T; 2: K^T, the decays and G;
-// 3: V.
+// the loads queue. Part 0: K and Q rows; 1: T; 2: the decays and G; 3: V.
 template <int PART, bool BF16, bool VEC>
 XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wave, int lr, int lg,
                       ScanOps<BF16, VEC>& L) {
     const int kh = h % 16;
     n = min(n, a.n_chunks - 1);  // the prefetch past the last chunk re-reads it
-    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * rec_bytes<BF16>();
+    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
     if constexpr (PART == 0) {
         const int tg = n * kChunk + 16 * wave + lr;  // A-operand row token
         L.ok = tg < a.T;
@@ -416,15 +393,6 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
             L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
         }
     } else if constexpr (PART == 2) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int a2 = 0; a2 < 2; ++a2) {
-                const int ko = ((16 * (2 * wave + a2) + lr) * 64 + 32 * ks + 8 * lg) * 2;
-                L.kt[a2][ks] = *(const h8*)(rec + kRecKT + ko);
-                if constexpr (!BF16) L.ktl[a2][ks] = *(const h8*)(rec + kRecKTLo + ko);
-            }
-        }
         const float* dec = (const float*)(rec + kRecDec);
         L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
         L.egc = *(const float4*)(dec + 64 + 16 * wave + 4 * lg);
@@ -468,6 +436,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sWh[kCols * TP], sWl[kCols * TP];  // (e^{G_C - G} U)^T
     // K rows of the chunk [t][i] (f16 hi, and lo for f32 rows): the A operands of P^T = K Q^T
     __shared__ __attribute__((aligned(16))) _Float16 sKh[64 * SP], sKl[BF16 ? 8 : 64 * SP];
+    // K^T [i][t] of the chunk, by chunk parity (read after the step's last
+    // barrier, so the next chunk writes the other one): the A operands of the
+    // state update
+    constexpr int KTP = 72;  // K^T rows (halves)
+    __shared__ __attribute__((aligned(16))) _Float16 sKTh[2][128 * KTP], sKTl[2][BF16 ? 8 : 128 * KTP];
 
     const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
     const uint32_t wg = xcd_remap(blockIdx.x, n_wg);  // column blocks of a head adjacent (one XCD)
@@ -492,10 +465,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     scan_load_all<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
     // One chunk: C holds its operands (loaded a chunk ahead), the next chunk's
     // operands are loaded into Nx part by part.
-    auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx) {
+    auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx, _Float16* kth, _Float16* ktl) {
         scan_load<0>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
 
-        // ---- the wave's K rows -> LDS (every wave forms its P from all of them)
+        // ---- the wave's K rows -> LDS, as rows (every wave forms its P from
+        //      all of them) and transposed (the state update's operands)
         h8 ak[4], aq[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -503,7 +477,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
             aq[ks] = decode8<BF16, VEC>(C.qw[ks], C.ok);
             const int ko = (16 * wave + lr) * SP + 32 * ks + 8 * lg;
             *(h8*)(sKh + ko) = ak[ks];
-            if constexpr (!BF16) *(h8*)(sKl + ko) = decode8_lo(C.kw[ks], C.ok);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kth[(32 * ks + 8 * lg + e) * KTP + 16 * wave + lr] = ak[ks][e];
+            if constexpr (!BF16) {
+                const h8 al = decode8_lo(C.kw[ks], C.ok);
+                *(h8*)(sKl + ko) = al;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ktl[(32 * ks + 8 * lg + e) * KTP + 16 * wave + lr] = al[e];
+            }
         }
 
         // ---- S (hi, lo) -> LDS as S^T [c][i]: the B operand rows of K S and Q S
@@ -634,10 +615,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const int bo = lr * TP + 32 * ks + 8 * lg;
-                const h8 wh = *(const h8*)(sWh + bo);
-                acc = mfma32(C.kt[a2][ks], wh, acc);
-                acc2 = mfma32(C.kt[a2][ks], *(const h8*)(sWl + bo), acc2);
-                if constexpr (!BF16) acc2 = mfma32(C.ktl[a2][ks], wh, acc2);
+                const int ko = (16 * (2 * wave + a2) + lr) * KTP + 32 * ks + 8 * lg;
+                const h8 wh = *(const h8*)(sWh + bo), kt = *(const h8*)(kth + ko);
+                acc = mfma32(kt, wh, acc);
+                acc2 = mfma32(kt, *(const h8*)(sWl + bo), acc2);
+                if constexpr (!BF16) acc2 = mfma32(*(const h8*)(ktl + ko), wh, acc2);
             }
             S[a2] = acc + acc2;
         }
@@ -648,10 +630,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     // iteration and never waits for the next chunk's operands early.
     int n = 0;
     for (; n + 1 < a.n_chunks; n += 2) {
-        chunk(n, ops[0], ops[1]);
-        chunk(n + 1, ops[1], ops[0]);
+        chunk(n, ops[0], ops[1], sKTh[0], sKTl[0]);
+        chunk(n + 1, ops[1], ops[0], sKTh[1], sKTl[1]);
     }
-    if (n < a.n_chunks) chunk(n, ops[0], ops[1]);
+    if (n < a.n_chunks) chunk(n, ops[0], ops[1], sKTh[0], sKTl[0]);
 
     // ---- final state (transposed layout: element (i, c) of head h at h*16384 + c*128 + i)
     float* so = a.state_out + (int64_t)b * (a.so_nb3 / 4) + (int64_t)h * 16384;
@@ -671,7 +653,8 @@ size_t gdn_chunked_workspace_bytes(int64_t T, int64_t B, int32_t slots, bool bf1
     const int64_t Tc = chunked_tokens(T, slots);
     if (Tc < 1) return 0;
     const int64_t nch = (Tc + kChunk - 1) / kChunk;
-    return (size_t)B * 32 * nch * (bf16_rows ? rec_bytes<true>() : rec_bytes<false>());
+    (void)bf16_rows;  // the record holds f16 planes whatever the row type
+    return (size_t)B * 32 * nch * kRecBytes;
 }
 
 bool gdn_chunked_available() { return true; }
