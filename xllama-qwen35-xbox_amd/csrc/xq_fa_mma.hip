@@ -155,8 +155,11 @@ XQ_DEV float xrow_sum(float x) {
 // kernel's explicit vmcnt waits order each DMA group before the reads of its
 // stage, and the asm's memory clobber keeps LDS reads on their side of them.
 // One wait state separates the m0 write from its use by the DMA. NT marks the
-// load non-temporal (KV rows are read once; measured 0.5-2 % faster on the decode
-// shapes, 1 % slower on the 32-pair verify tile, which keeps ordinary loads).
+// load non-temporal: KV rows are read once (2 % faster on the 4k f16 decode).
+// Only records that are whole 128-byte lines take it: a line shared by two
+// heads' records (272-byte q8_0 records) is otherwise fetched once into L2 for
+// both, and non-temporal loads fetch it twice (+11 % HBM traffic, no faster).
+// The 32-pair verify tile keeps ordinary loads (1 % slower with them).
 template <int CS, bool NT = false>
 XQ_DEV void lds_dma(const uint8_t* base, uint32_t off, uint8_t* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
@@ -262,7 +265,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             const uint8_t* bt = base + (int64_t)t0 * nb1;
 #pragma unroll
             for (int i = 0; i < NIS; ++i)
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS, MT == 1>(bt, off[i], dst + i * 64 * CS);
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS, MT == 1 && REC % 128 == 0>(bt, off[i], dst + i * 64 * CS);
         } else {
             // rows from tr = min(t0, r_end - 1); lane rows clamp to r_end - 1, so
             // every offset is non-negative and below 16 rows (the whole slice
@@ -273,7 +276,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             for (int i = 0; i < NIS; ++i) {
                 const int row = min(t0 + crow[i], r_end - 1);
                 const uint32_t o = off[i] + (uint32_t)(row - tr - crow[i]) * (uint32_t)nb1;
-                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS, MT == 1>(bt, o, dst + i * 64 * CS);
+                if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS, MT == 1 && REC % 128 == 0>(bt, o, dst + i * 64 * CS);
             }
         }
     };
