@@ -186,6 +186,23 @@ xq_status xq_fa_range(const float* q, const int32_t* positions, int32_t n_q, int
                       int32_t split_mode, float* out, float* lse, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* Merge of position-split results: n_parts results of the same rows
+ * (query, head) over disjoint KV ranges, each OUT [rows][head_dim] F32 and
+ * natural-log LSE [rows] F32 as xq_fa_range or xq_flash_attn_ext return them
+ * (an empty range is O = 0, LSE = -inf), into OUT and LSE over the union:
+ * M = max LSE_p over the parts with LSE_p != -inf,
+ * OUT = sum_p OUT_p e^(LSE_p - M) / sum_p e^(LSE_p - M), LSE = M + ln(sum),
+ * accumulated in part order. This is the merge a caller applies after
+ * splitting the KV rows between engines or devices (the result contract of
+ * uwp/rkva/remote-attn-protocol.h:228-231; poisoning as the split reducer,
+ * shaders/rkva/rkva_range_reduce_opt.hlsl:39-56,126-132: a participating
+ * NaN or +inf LSE, or a non-finite merged value, makes the row NaN). No
+ * participating part gives O = 0, LSE = -inf.
+ *   parts_out [n_parts][rows][head_dim], parts_lse [n_parts][rows] (device)
+ *   out [rows][head_dim], lse [rows] (device); 1 <= head_dim <= 512. */
+xq_status xq_fa_lse_merge(const float* parts_out, const float* parts_lse, int32_t n_parts,
+                          int64_t rows, int32_t head_dim, float* out, float* lse, void* stream);
+
 /* Split count the policy picks for a KV length (host-side, pure; AUTO is
  * evaluated for one sequence and one KV head). */
 int32_t xq_fa_split_count(int64_t kv_len, int32_t split_mode);

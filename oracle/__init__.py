@@ -82,6 +82,7 @@ def load() -> ctypes.CDLL:
         "xo_q4_mq_split": (None, [u32, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]),
         "xo_range_attn_partials": (ctypes.c_int, [P, P, i32, i32, P, P, i32, i32, i32, i32, i32, f32, i32, P]),
         "xo_range_reduce": (ctypes.c_int, [P, i32, i32, i32, i32, P, P]),
+        "xo_lse_merge": (ctypes.c_int, [P, P, i32, ctypes.c_int64, i32, P, P]),
         "xo_gated_delta_net": (ctypes.c_int, [T, T, T, T, T, T, T, i32, ctypes.c_int]),
         "xo_gated_delta_net_f64": (ctypes.c_int, [T, T, T, T, T, T, P, i32, ctypes.c_int]),
         "xo_kv_store": (ctypes.c_int, [P, P, i32, i32, i32, i32, i32, P, i32]),
@@ -288,6 +289,18 @@ def range_reduce(parts: np.ndarray, head_dim: int, poison: bool):
     out = np.empty((n_qh, head_dim), np.float32)
     lse = np.empty((n_qh,), np.float32)
     load().xo_range_reduce(_ptr(parts), n_qh, head_dim, split_k, int(poison), _ptr(out), _ptr(lse))
+    return out, lse
+
+
+def lse_merge(parts_out: np.ndarray, parts_lse: np.ndarray):
+    """parts_out [n_parts, rows, D], parts_lse [n_parts, rows] -> (out [rows, D], lse [rows])."""
+    parts_out = np.ascontiguousarray(parts_out, np.float32)
+    parts_lse = np.ascontiguousarray(parts_lse, np.float32)
+    n_parts, rows, D = parts_out.shape
+    assert parts_lse.shape == (n_parts, rows)
+    out = np.empty((rows, D), np.float32)
+    lse = np.empty((rows,), np.float32)
+    load().xo_lse_merge(_ptr(parts_out), _ptr(parts_lse), n_parts, rows, D, _ptr(out), _ptr(lse))
     return out, lse
 
 

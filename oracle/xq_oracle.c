@@ -756,6 +756,63 @@ int xo_range_reduce(const float* partials, int32_t n_qh, int32_t D, int32_t spli
     return 0;
 }
 
+/* Merge of position-split range results: parts p = 0..n_parts-1 hold OUT
+ * [rows][D] and natural-log LSE [rows] of the same (query, head) rows over
+ * disjoint KV ranges (the result contract of uwp/rkva/remote-attn-protocol.h:
+ * 228-231: an empty range gives O = 0, LSE = -inf). A part takes part when its
+ * LSE is not -inf (the reducer's den != 0); weights e^{LSE_p - M}, M the
+ * largest such LSE, accumulate in part order; a participating NaN / +inf LSE
+ * or a non-finite result poisons the row with NaN, as
+ * shaders/rkva/rkva_range_reduce_opt.hlsl:39-56,126-132 does for splits. */
+int xo_lse_merge(const float* parts_out, const float* parts_lse, int32_t n_parts, int64_t rows,
+                 int32_t D, float* out, float* lse) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float* o = out + (size_t)r * D;
+        int invalid = 0, any = 0;
+        float M = -FLT_MAX;
+        for (int32_t p = 0; p < n_parts; ++p) {
+            const float l = parts_lse[(size_t)p * rows + r];
+            if (l == -INFINITY) continue;
+            if (!isfinite(l))
+                invalid = 1;
+            else {
+                any = 1;
+                if (l > M) M = l;
+            }
+        }
+        if (!invalid && !any) {
+            for (int32_t d = 0; d < D; ++d) o[d] = 0.0f;
+            lse[r] = -INFINITY;
+            continue;
+        }
+        float sum = 0.0f;
+        if (!invalid)
+            for (int32_t p = 0; p < n_parts; ++p) {
+                const float l = parts_lse[(size_t)p * rows + r];
+                if (l != -INFINITY) sum = sum + expf(l - M);
+            }
+        const float inv = invalid ? 0.0f : 1.0f / sum;
+        const float lv = invalid ? NAN : M + logf(sum);
+        if (!isfinite(lv) || !isfinite(inv)) invalid = 1;
+        for (int32_t d = 0; d < D && !invalid; ++d) {
+            float acc = 0.0f;
+            for (int32_t p = 0; p < n_parts; ++p) {
+                const float l = parts_lse[(size_t)p * rows + r];
+                if (l != -INFINITY) acc = acc + parts_out[((size_t)p * rows + r) * D + d] * expf(l - M);
+            }
+            o[d] = acc * inv;
+            if (!isfinite(o[d])) invalid = 1;
+        }
+        if (invalid) {
+            for (int32_t d = 0; d < D; ++d) o[d] = NAN;
+            lse[r] = NAN;
+        } else {
+            lse[r] = lv;
+        }
+    }
+    return 0;
+}
+
 /* ======================================================================
  * gated delta net
  * ==================================================================== */

@@ -84,6 +84,11 @@ int xo_range_attn_partials(const float* q, const int32_t* positions, int32_t n_q
 int xo_range_reduce(const float* partials, int32_t n_qh, int32_t head_dim, int32_t split_k,
                     int32_t poison, float* out, float* lse);
 
+/* Merge of position-split range results (OUT [rows][D] + LSE [rows] per part,
+ * parts over disjoint KV ranges) in part order, with the reducer's poisoning. */
+int xo_lse_merge(const float* parts_out, const float* parts_lse, int32_t n_parts, int64_t rows,
+                 int32_t D, float* out, float* lse);
+
 /* ---- gated delta net ---- */
 
 /* Sequential recurrence in the order of d3d12_gdn_emulate

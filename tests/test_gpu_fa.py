@@ -259,3 +259,60 @@ def test_fa_graph_replays_match_eager(torch_gpu):
         assert np.array_equal(d.to_host_bytes(), eager), f"replay {rep} differs"
         xqattn.flash_attn_ext(q, k, v, m, None, d, p, workspace=ws)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_lse_merge_matches_oracle(torch_gpu):
+    """xq_fa_lse_merge against the oracle's merge: empty pieces (LSE -inf, their
+    O never read), a row no piece sees, and poisoned rows (NaN LSE, NaN value)."""
+    torch = torch_gpu
+    rng = np.random.default_rng(11)
+    n_parts, rows, D = 6, 200, 256
+    po = rng.standard_normal((n_parts, rows, D)).astype(np.float32)
+    pl = (rng.standard_normal((n_parts, rows)) * 10).astype(np.float32)
+    pl[2, ::4] = -np.inf
+    po[2, ::4] = np.inf
+    pl[:, 9] = -np.inf
+    pl[3, 11] = np.nan
+    po[4, 13, 7] = np.nan
+    want, wlse = oracle.lse_merge(po, pl)
+    case_note("lse merge vs oracle")
+    out = torch.empty(rows, D, dtype=torch.float32, device="cuda")
+    lse = torch.empty(rows, dtype=torch.float32, device="cuda")
+    xqattn.fa_lse_merge(torch.from_numpy(po).cuda(), torch.from_numpy(pl).cuda(), out, lse)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want, atol=1e-6, rtol=1e-6, what="merged O")
+    assert_close(lse.cpu().numpy(), wlse, atol=1e-6, rtol=1e-6, what="merged LSE")
+
+
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0])
+def test_range_pieces_merged_equal_whole_range(torch_gpu, kv_type):
+    """Range attention over two pieces of the KV rows (the second with its origin
+    moved by the cut), merged with xq_fa_lse_merge, equals range attention over
+    all rows: the exchange a split of the KV rows across devices needs."""
+    torch = torch_gpu
+    n_head, hkv, D, origin, active, cut = 24, 4, 256, 102400, 5000, 1777
+    kraw = oracle.quantize(kv_type, wl.normal(71, (active, hkv, D)))
+    vraw = oracle.quantize(kv_type, wl.normal(72, (active, hkv, D)))
+    positions = np.array([origin + active - 1, origin + 1000, origin - 5, origin + 3000], np.int32)
+    q = wl.normal(73, (positions.size, n_head, D))
+    n_q = positions.size
+    dq, dpos = torch.from_numpy(q).cuda(), torch.from_numpy(positions).cuda()
+    kd, vd = torch.from_numpy(kraw).cuda(), torch.from_numpy(vraw).cuda()
+
+    def run(a, b):
+        out = torch.empty(n_q * n_head * D, dtype=torch.float32, device="cuda")
+        lse = torch.empty(n_q * n_head, dtype=torch.float32, device="cuda")
+        xqattn.fa_range(dq, dpos, n_head, kd[a:b].contiguous().reshape(-1), vd[a:b].contiguous().reshape(-1),
+                        hkv, D, kv_type, origin + a, b - a, 1.0 / 16, out, lse)
+        return out.reshape(n_q * n_head, D), lse
+
+    case_note(f"range pieces + merge {wl.TYPE_NAME[kv_type]}")
+    whole, wlse = run(0, active)
+    p0, l0 = run(0, cut)
+    p1, l1 = run(cut, active)
+    out = torch.empty(n_q * n_head, D, dtype=torch.float32, device="cuda")
+    lse = torch.empty(n_q * n_head, dtype=torch.float32, device="cuda")
+    xqattn.fa_lse_merge(torch.stack([p0, p1]), torch.stack([l0, l1]), out, lse)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), whole.cpu().numpy(), atol=1e-4, rtol=1e-4, what="merged pieces vs whole")
+    assert_close(lse.cpu().numpy(), wlse.cpu().numpy(), atol=1e-5, rtol=1e-6, what="merged LSE vs whole")

@@ -310,6 +310,20 @@ static void range_descs(int32_t n_q, int32_t n_head, int32_t n_head_kv, int32_t 
                     {4, (size_t)D * 4, (size_t)n_head * D * 4, (size_t)n_q * n_head * D * 4}, out};
 }
 
+xq_status xq_fa_lse_merge(const float* parts_out, const float* parts_lse, int32_t n_parts,
+                          int64_t rows, int32_t head_dim, float* out, float* lse, void* stream) {
+    if (!parts_out || !parts_lse || !out || !lse) return fail(XQ_ERR_BAD_ARG, "null pointer");
+    if (n_parts < 1 || rows < 1 || head_dim < 1) return fail(XQ_ERR_BAD_ARG, "bad merge sizes");
+    if (head_dim > 512) return fail(XQ_ERR_UNSUPPORTED, "head dim above 512");
+    if (rows > 0x7fffffff) return fail(XQ_ERR_UNSUPPORTED, "more than 2^31 rows");
+    for (const void* p : {(const void*)parts_out, (const void*)parts_lse, (const void*)out, (const void*)lse})
+        if (!aligned(p, 4)) return fail(XQ_ERR_UNSUPPORTED, "misaligned pointer");
+    const hipError_t e =
+        xq::fa_lse_merge_launch(parts_out, parts_lse, n_parts, rows, head_dim, out, lse, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(XQ_ERR_HIP, "fa_lse_merge launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
 xq_status xq_fa_range_workspace(int32_t n_q, int32_t n_head, int32_t n_head_kv, int32_t head_dim,
                                 int32_t kv_type, int32_t active, int32_t split_mode, size_t* bytes) {
     if (!bytes || n_q < 1 || n_head < 1 || n_head_kv < 1 || active < 0)

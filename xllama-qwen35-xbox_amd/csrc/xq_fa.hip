@@ -738,6 +738,78 @@ __global__ __launch_bounds__(256) void fa_mask_pack(const uint8_t* __restrict__ 
     }
 }
 
+// Merge of position-split results: one wave per row, lane owns dims
+// lane + 64 m. Every lane walks the parts in order (uniform loads of the LSEs).
+__global__ __launch_bounds__(64) void fa_lse_merge(const float* __restrict__ po, const float* __restrict__ pl,
+                                                   int n_parts, int64_t rows, int d, float* __restrict__ out,
+                                                   float* __restrict__ lse) {
+    constexpr int kMaxPerLane = 8;  // d <= 512
+    const int64_t r = blockIdx.x;
+    const int lane = threadIdx.x;
+    bool bad = false, any = false;
+    float M = -3.402823466e38f;
+    for (int p = 0; p < n_parts; ++p) {
+        const float l = pl[(int64_t)p * rows + r];
+        if (l == -INFINITY) continue;
+        if (!isfinite(l)) {
+            bad = true;
+        } else {
+            any = true;
+            M = fmaxf(M, l);
+        }
+    }
+    float* o = out + r * d;
+    if (!bad && !any) {  // every range empty
+        for (int i = lane; i < d; i += 64) o[i] = 0.0f;
+        if (lane == 0) lse[r] = -INFINITY;
+        return;
+    }
+    float sum = 0.0f;
+    if (!bad)
+        for (int p = 0; p < n_parts; ++p) {
+            const float l = pl[(int64_t)p * rows + r];
+            if (l != -INFINITY) sum = sum + expf(l - M);
+        }
+    const float inv = bad ? 0.0f : 1.0f / sum;
+    const float lv = bad ? NAN : M + logf(sum);
+    bad = bad || !isfinite(lv) || !isfinite(inv);
+    float acc[kMaxPerLane];
+#pragma unroll
+    for (int m = 0; m < kMaxPerLane; ++m) acc[m] = 0.0f;
+    if (!bad)
+        for (int p = 0; p < n_parts; ++p) {
+            const float l = pl[(int64_t)p * rows + r];
+            if (l == -INFINITY) continue;
+            const float w = expf(l - M);
+            const float* src = po + ((int64_t)p * rows + r) * d;
+#pragma unroll
+            for (int m = 0; m < kMaxPerLane; ++m) {
+                const int i = lane + 64 * m;
+                if (i < d) acc[m] = acc[m] + src[i] * w;
+            }
+        }
+    bool lane_bad = false;
+#pragma unroll
+    for (int m = 0; m < kMaxPerLane; ++m) {
+        acc[m] = acc[m] * inv;
+        if (lane + 64 * m < d && !isfinite(acc[m])) lane_bad = true;
+    }
+    bad = bad || __any(lane_bad);
+#pragma unroll
+    for (int m = 0; m < kMaxPerLane; ++m) {
+        const int i = lane + 64 * m;
+        if (i < d) o[i] = bad ? NAN : acc[m];
+    }
+    if (lane == 0) lse[r] = bad ? NAN : lv;
+}
+
+hipError_t fa_lse_merge_launch(const float* parts_out, const float* parts_lse, int n_parts, int64_t rows, int d,
+                               float* out, float* lse, hipStream_t stream) {
+    launch("fa_lse_merge", fa_lse_merge, dim3((uint32_t)rows), dim3(64), stream, parts_out, parts_lse, n_parts, rows,
+           d, out, lse);
+    return hipGetLastError();
+}
+
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits) {
     size_t bytes = align256(qimg_bytes(n_rows, d, qk_mode, kt));
     if (n_splits > 1) {

@@ -81,6 +81,8 @@ struct FaLaunch {
 };
 
 size_t fa_workspace_bytes(int64_t n_rows, int d, int qk_mode, int kt, int n_splits);
+hipError_t fa_lse_merge_launch(const float* parts_out, const float* parts_lse, int n_parts, int64_t rows, int d,
+                               float* out, float* lse, hipStream_t stream);
 // Extra workspace after fa_workspace_bytes for a mask whose rows the
 // matrix-core engine must re-lay (reserved whenever a mask is given).
 size_t fa_mask_pack_bytes(const xq_tensor* mask, int64_t L, int n_q);

@@ -36,7 +36,7 @@ ENGINE_AUTO, ENGINE_MFMA, ENGINE_VALU = 0, 1, 2
 
 EXPORTS = (
     "xq_supports_flash_attn_ext", "xq_flash_attn_ext_workspace", "xq_flash_attn_ext",
-    "xq_fa_range_workspace", "xq_fa_range", "xq_fa_split_count", "xq_fa_split_rows",
+    "xq_fa_range_workspace", "xq_fa_range", "xq_fa_lse_merge", "xq_fa_split_count", "xq_fa_split_rows",
     "xq_supports_gated_delta_net", "xq_gated_delta_net_workspace", "xq_gated_delta_net",
     "xq_kv_store", "xq_kv_record_bytes", "xq_last_error", "xq_abi_version",
     "xq_profile_enable", "xq_profile_reset", "xq_profile_read",
@@ -92,6 +92,7 @@ def load() -> ctypes.CDLL:
         "xq_flash_attn_ext": (i32, [T, T, T, T, T, T, P, FP, P, sz, P]),
         "xq_fa_range_workspace": (i32, [i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(sz)]),
         "xq_fa_range": (i32, [P, P, i32, i32, P, P, i32, i32, i32, i32, i32, f32, i32, P, P, P, sz, P]),
+        "xq_fa_lse_merge": (i32, [P, P, i32, i64, i32, P, P, P]),
         "xq_fa_split_count": (i32, [i64, i32]),
         "xq_fa_split_rows": (i64, [i64, i32]),
         "xq_supports_gated_delta_net": (ctypes.c_int, [T, T, T, T, T, T, T, i32, i32]),
@@ -241,6 +242,14 @@ def fa_range(q, positions, n_head, k, v, n_head_kv, head_dim, kv_type, origin, a
                            out.data_ptr(), lse.data_ptr(), ctypes.c_void_p(wp), wn, _stream(stream)),
            "fa_range")
     return ws
+
+
+def fa_lse_merge(parts_out, parts_lse, out, lse, stream=None):
+    """Merge position-split results: parts_out [n_parts, rows, D], parts_lse
+    [n_parts, rows] (device tensors) into out [rows, D], lse [rows]."""
+    n_parts, rows, d = parts_out.shape
+    _check(load().xq_fa_lse_merge(parts_out.data_ptr(), parts_lse.data_ptr(), n_parts, rows, d, out.data_ptr(),
+                                  lse.data_ptr(), _stream(stream)), "fa_lse_merge")
 
 
 def split_count(kv_len: int, split_mode: int = SPLIT_AUTO) -> int:
