@@ -27,6 +27,7 @@ import pathlib
 import numpy as np
 
 from xqattn import workloads as wl
+from xqattn import xfa1
 
 GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
 SENTINEL = np.float32(1e30)
@@ -61,6 +62,35 @@ def fa_tensors(meta: dict, a: dict):
     sinks = wl.f32_tensor(a["sinks"], (meta["H"], 1, 1, 1)) if "sinks" in a else None
     B, NQ, H, _ = a["q"].shape
     return q, k, v, mask, sinks, wl.fa_dst_tensor(B, NQ, H, D)
+
+
+def cache_view(raw: np.ndarray, typ: int, d: int, spare: int, seed: int) -> wl.HostTensor:
+    """raw records [B, L, Hkv, rec] placed in a cache of L + spare rows per
+    sequence (junk in the spare rows) -> the ggml view of the first L rows."""
+    B, L, Hkv, rec = raw.shape
+    cache = np.random.default_rng(seed).integers(0, 256, (B, L + spare, Hkv, rec), dtype=np.uint8)
+    cache[:, :L] = raw
+    nb = (wl.TYPE_SIZE[typ], Hkv * rec, rec, (L + spare) * Hkv * rec)
+    span = xfa1.span_bytes(typ, (d, L, Hkv, B), nb)
+    return wl.HostTensor(typ, (d, L, Hkv, B), nb, cache.reshape(-1)[:span].copy())
+
+
+def fa_capture(path, out_dir, spare=24):
+    """Write a multi-query FA fixture as an XFA1 capture, with ggml-like op ids
+    and names -> (meta, arrays, (q, k, v, mask, output) host tensors, file)."""
+    meta, a = load(path)
+    q, k, v, m, s, dst = fa_tensors(meta, a)
+    assert s is None
+    kt, D = meta["kv_type"], meta["D"]
+    k = cache_view(a["k"], kt, D, spare, 1)
+    v = cache_view(a["v"], kt, D, spare, 2)
+    out = wl.HostTensor(wl.F32, dst.ne, dst.nb, np.ascontiguousarray(a["out"]).reshape(-1).view(np.uint8))
+    cap = pathlib.Path(out_dir) / f"{path.stem}.xfa1"
+    xfa1.write(cap, dict(q=q, k=k, v=v, mask=m, output=out),
+               ops=dict(q=34, k=33, v=33, mask=0, output=74),
+               names=dict(q="q-0", k="cache_k_l3 (view)", v="cache_v_l3 (view)", mask="attn_inp_kq_mask",
+                          output="__fattn__-3"))
+    return meta, a, (q, k, v, m, out), cap
 
 
 # ---------------------------------------------------------------------------
