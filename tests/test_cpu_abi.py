@@ -17,7 +17,7 @@ import xqattn
 from conftest import ROOT
 from xqattn import workloads as wl
 
-HEADER = ROOT / "include" / "xq_attn.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def lib():
@@ -25,18 +25,21 @@ def lib():
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(xq_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(xq_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_loads_and_exports_header():
     l = lib()
+    assert [h.name for h in HEADERS] == ["xq_attn.h", "xq_ggml_backend.h"]
     names = declared_functions()
-    assert len(names) >= 17
+    assert len(names) >= 24
     for n in names:
-        assert hasattr(l, n), f"{n} declared in xq_attn.h but not exported"
-    assert set(xqattn.EXPORTS) <= set(names)
+        assert hasattr(l, n), f"{n} declared in include/ but not exported"
+    assert set(xqattn.EXPORTS) == set(names)
     assert l.xq_abi_version() == 1
     assert l.xq_last_error() == b""
 

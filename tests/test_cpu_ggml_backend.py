@@ -1,0 +1,85 @@
+"""The ggml-backend face of the library on the host (no GPU calls): the node
+descriptor's layout, op_params packing as ggml's graph constructors write it,
+and the pure supports_op predicate (src/bridge/ggml_d3d12.cpp:2331-2353 for
+the predicate's role, :77-109 for the GDN operand rules)."""
+import ctypes
+import struct
+
+import pytest
+
+import xqattn
+from test_cpu_abi import _desc, _fa_descs
+from xqattn import workloads as wl
+
+
+def test_node_struct_layout():
+    # int32 op, int32 flags, 16 int32 op_params, xq_tensor dst (80 bytes), 10 pointers
+    assert ctypes.sizeof(xqattn.XqTensor) == 4 + 4 + 32 + 32 + 8
+    assert xqattn.XqGgmlNode.dst.offset == 4 + 4 + 64
+    assert xqattn.XqGgmlNode.src.offset == 72 + 80
+    assert ctypes.sizeof(xqattn.XqGgmlNode) == 72 + 80 + 80
+    assert ctypes.sizeof(xqattn.XqGgmlBackendParams) == 32
+
+
+def test_fa_op_params_are_ggml_float_bits():
+    q, k, v, m, dst = _fa_descs()
+    n = xqattn.GgmlNode.flash_attn_ext(q, k, v, m, None, dst, 1 / 16, max_bias=8.0, softcap=30.0, prec=10)
+    st = n.struct()
+    words = list(st.op_params)
+    assert words[:4] == [struct.unpack("<i", struct.pack("<f", x))[0] for x in (1 / 16, 8.0, 30.0)] + [10]
+    assert words[4:] == [0] * 12
+    assert st.op == xqattn.OP_FLASH_ATTN_EXT and st.flags == xqattn.GGML_FLAG_COMPUTE
+    assert bool(st.src[3]) and not bool(st.src[4]) and not bool(st.src[5])
+    assert st.src[1].contents.type == wl.Q8_0 and st.src[1].contents.ne[1] == 32768
+
+
+@pytest.mark.parametrize("kv", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2])
+def test_supports_op_fa_matches_direct_predicate(kv):
+    for D in (128, 256):
+        q, k, v, m, dst = _fa_descs(kv=kv, D=D)
+        node = xqattn.GgmlNode.flash_attn_ext(q, k, v, m, None, dst, 1 / 16)
+        assert xqattn.ggml_supports_op(node)
+        # a sixth source is not part of FLASH_ATTN_EXT's contract
+        node.srcs.append(m)
+        assert not xqattn.ggml_supports_op(node)
+    q, k, v, m, dst = _fa_descs(D=64)  # head dim outside the kernels
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode.flash_attn_ext(q, k, v, m, None, dst, 0.125))
+    q, k, v, m, dst = _fa_descs()
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode.flash_attn_ext(None, k, v, m, None, dst, 0.125))
+
+
+def _gdn_descs(T=1, B=8, slots=1):
+    q = _desc(wl.F32, (128, 16, T, B))
+    k = _desc(wl.F32, (128, 16, T, B))
+    v = _desc(wl.F32, (128, 32, T, B))
+    g = _desc(wl.F32, (1, 32, T, B))
+    beta = _desc(wl.F32, (1, 32, T, B))
+    s = _desc(wl.F32, (128, 128, 32, B))
+    dst = _desc(wl.F32, (4096, T + slots * 128, B, 1))
+    return q, k, v, g, beta, s, dst
+
+
+def test_supports_op_gdn_contract():
+    q, k, v, g, beta, s, dst = _gdn_descs()
+    ok = xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, 1)
+    assert xqattn.ggml_supports_op(ok)
+    assert list(ok.struct().op_params[:2]) == [1, 0]
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, 1, raw_gates=1))
+    q5, k5, v5, g5, b5, s5, d5 = _gdn_descs(T=5, B=1, slots=5)
+    assert xqattn.ggml_supports_op(xqattn.GgmlNode.gated_delta_net(q5, k5, v5, g5, b5, s5, d5, 5))
+    q18, k18, v18, g18, b18, s18, d18 = _gdn_descs(T=1, B=1, slots=18)
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode.gated_delta_net(q18, k18, v18, g18, b18, s18, d18, 18))
+    # the rows-indexed mode (src[6..8]) is outside the contract
+    rows = xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, 1)
+    rows.srcs += [q]
+    assert not xqattn.ggml_supports_op(rows)
+    missing = xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, None, dst, 1)
+    assert not xqattn.ggml_supports_op(missing)
+
+
+def test_supports_op_noop_and_other_kinds():
+    dst = _desc(wl.F32, (4096, 1, 1, 1))
+    assert xqattn.ggml_supports_op(xqattn.GgmlNode.noop(dst))
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode(xqattn.OP_OTHER, dst))
+    assert not xqattn.ggml_supports_op(xqattn.GgmlNode(7, dst))
+    assert xqattn.load().xq_ggml_supports_op(None) == 0

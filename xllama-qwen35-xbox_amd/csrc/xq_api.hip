@@ -211,6 +211,15 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
 
+namespace xq {
+
+xq_status set_error(xq_status st, const char* msg) {
+    g_last_error = msg;
+    return st;
+}
+
+}  // namespace xq
+
 extern "C" {
 
 int32_t xq_abi_version(void) { return XQ_ABI_VERSION; }

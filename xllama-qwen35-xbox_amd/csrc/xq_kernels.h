@@ -12,6 +12,9 @@
 
 namespace xq {
 
+// Sets the calling thread's xq_last_error message and returns st.
+xq_status set_error(xq_status st, const char* msg);
+
 // Per-kernel device timing. While profiling is enabled (and the stream is not
 // being captured into a graph), launch() hands the kernel a start/stop HIP
 // event pair that the dispatch itself records at the kernel's first wave and

@@ -40,6 +40,8 @@ EXPORTS = (
     "xq_supports_gated_delta_net", "xq_gated_delta_net_workspace", "xq_gated_delta_net",
     "xq_kv_store", "xq_kv_record_bytes", "xq_last_error", "xq_abi_version",
     "xq_profile_enable", "xq_profile_reset", "xq_profile_read",
+    "xq_ggml_backend_init", "xq_ggml_backend_free", "xq_ggml_backend_name", "xq_ggml_backend_stream",
+    "xq_ggml_backend_workspace_bytes", "xq_ggml_supports_op", "xq_ggml_graph_compute",
 )
 
 
@@ -68,6 +70,31 @@ class XqFaParams(ctypes.Structure):
         ("split_mode", ctypes.c_int32),
         ("engine", ctypes.c_int32),
         ("reserved", ctypes.c_int32 * 2),
+    ]
+
+
+GGML_MAX_SRC, GGML_MAX_OP_PARAMS, GGML_FLAG_COMPUTE = 10, 16, 1
+OP_NOOP, OP_FLASH_ATTN_EXT, OP_GATED_DELTA_NET, OP_OTHER = 0, 1, 2, 3
+
+
+class XqGgmlNode(ctypes.Structure):
+    """xq_ggml_node: one ggml graph node as a backend binding copies it out."""
+    _fields_ = [
+        ("op", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("op_params", ctypes.c_int32 * GGML_MAX_OP_PARAMS),
+        ("dst", XqTensor),
+        ("src", ctypes.POINTER(XqTensor) * GGML_MAX_SRC),
+    ]
+
+
+class XqGgmlBackendParams(ctypes.Structure):
+    _fields_ = [
+        ("fa_qk_policy", ctypes.c_int32),
+        ("fa_split_mode", ctypes.c_int32),
+        ("fa_engine", ctypes.c_int32),
+        ("gdn_mode", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 4),
     ]
 
 
@@ -106,6 +133,13 @@ def load() -> ctypes.CDLL:
         "xq_profile_reset": (None, []),
         "xq_profile_read": (i32, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64), i32]),
+        "xq_ggml_backend_init": (P, [i32, ctypes.POINTER(XqGgmlBackendParams)]),
+        "xq_ggml_backend_free": (None, [P]),
+        "xq_ggml_backend_name": (ctypes.c_char_p, [P]),
+        "xq_ggml_backend_stream": (P, [P]),
+        "xq_ggml_backend_workspace_bytes": (sz, [P]),
+        "xq_ggml_supports_op": (ctypes.c_int, [ctypes.POINTER(XqGgmlNode)]),
+        "xq_ggml_graph_compute": (i32, [P, ctypes.POINTER(XqGgmlNode), i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -337,3 +371,102 @@ def profile_read(max_entries: int = 32) -> dict:
         nm = names.raw[32 * i: 32 * (i + 1)].split(b"\0", 1)[0].decode()
         out[nm] = (ms[i], cnt[i])
     return out
+
+
+# ---------------------------------------------------------------------------
+# ggml backend face (include/xq_ggml_backend.h)
+# ---------------------------------------------------------------------------
+
+class GgmlNode:
+    """A ggml node for the backend: op kind, op_params words, dst and sources.
+
+    The constructors pack op_params as ggml's own graph constructors do:
+    ``ggml_flash_attn_ext`` stores (scale, max_bias, logit_softcap) as float
+    bits and ``ggml_flash_attn_ext_set_prec`` the precision in word 3;
+    ``ggml_gated_delta_net`` stores the snapshot slots in word 0 and the
+    raw-gate flag in word 1 (src/bridge/ggml_d3d12.cpp:77-83)."""
+
+    def __init__(self, op, dst, srcs=(), op_params=(), compute=True):
+        self.op, self.dst, self.srcs = op, dst, list(srcs)
+        self.op_params = list(op_params) + [0] * (GGML_MAX_OP_PARAMS - len(op_params))
+        self.compute = compute
+        self._keep = []
+
+    @staticmethod
+    def f32_bits(x) -> int:
+        import struct
+        return struct.unpack("<i", struct.pack("<f", float(x)))[0]
+
+    @classmethod
+    def flash_attn_ext(cls, q, k, v, mask, sinks, dst, scale, max_bias=0.0, softcap=0.0, prec=0, compute=True):
+        words = [cls.f32_bits(scale), cls.f32_bits(max_bias), cls.f32_bits(softcap), int(prec)]
+        return cls(OP_FLASH_ATTN_EXT, dst, [q, k, v, mask, sinks], words, compute)
+
+    @classmethod
+    def gated_delta_net(cls, q, k, v, g, beta, state, dst, slots, raw_gates=0, compute=True):
+        return cls(OP_GATED_DELTA_NET, dst, [q, k, v, g, beta, state], [int(slots), int(raw_gates)], compute)
+
+    @classmethod
+    def noop(cls, dst):
+        return cls(OP_NOOP, dst)
+
+    def struct(self) -> XqGgmlNode:
+        n = XqGgmlNode()
+        n.op = self.op
+        n.flags = GGML_FLAG_COMPUTE if self.compute else 0
+        for i, w in enumerate(self.op_params):
+            n.op_params[i] = w
+        n.dst = self.dst.desc() if hasattr(self.dst, "desc") else self.dst
+        self._keep = []
+        for i, s in enumerate(self.srcs):
+            if s is None:
+                continue
+            d = s.desc() if hasattr(s, "desc") else s
+            self._keep.append(d)
+            n.src[i] = ctypes.pointer(d)
+        return n
+
+
+def ggml_supports_op(node: GgmlNode) -> bool:
+    """dev_supports_op for this backend (pure; no GPU needed)."""
+    st = node.struct()
+    return bool(load().xq_ggml_supports_op(ctypes.byref(st)))
+
+
+class GgmlBackend:
+    """The backend object: its own HIP stream, a grow-only workspace, and a
+    synchronous ``graph_compute`` over ``GgmlNode`` lists."""
+
+    def __init__(self, device=0, fa_qk_policy=QK_CONSISTENT, fa_split_mode=SPLIT_AUTO,
+                 fa_engine=ENGINE_AUTO, gdn_mode=GDN_AUTO):
+        lib = load()
+        p = XqGgmlBackendParams()
+        p.fa_qk_policy, p.fa_split_mode, p.fa_engine, p.gdn_mode = fa_qk_policy, fa_split_mode, fa_engine, gdn_mode
+        self._h = lib.xq_ggml_backend_init(device, ctypes.byref(p))
+        if not self._h:
+            raise XqError(5, "ggml_backend_init", lib.xq_last_error().decode())
+
+    @property
+    def name(self) -> str:
+        return load().xq_ggml_backend_name(self._h).decode()
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(load().xq_ggml_backend_workspace_bytes(self._h))
+
+    def graph_compute(self, nodes):
+        arr = (XqGgmlNode * max(1, len(nodes)))()
+        for i, n in enumerate(nodes):
+            arr[i] = n.struct()
+        _check(load().xq_ggml_graph_compute(self._h, arr, len(nodes)), "ggml_graph_compute")
+
+    def free(self):
+        if self._h:
+            load().xq_ggml_backend_free(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
