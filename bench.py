@@ -70,6 +70,9 @@ def make_fa_sets(torch, xq, wl, cfg, n_sets, seed=0):
         qt = torch.randn((B, NQ, H, D), generator=gen, device="cuda", dtype=torch.float32)
         q = xq.DevTensor(wl.F32, (D, NQ, H, B), (4, H * D * 4, D * 4, NQ * H * D * 4), qt)
         mt = torch.zeros((B, NQ, L), dtype=torch.float16, device="cuda")  # all-visible, one row per sequence
+        if cfg.causal_prefix is not None:  # query i sees rows <= prefix + i
+            for i in range(NQ):
+                mt[:, i, cfg.causal_prefix + i + 1:] = float("-inf")
         m = xq.DevTensor(wl.F16, (L, NQ, 1, B), (2, L * 2, NQ * L * 2, NQ * L * 2), mt)
         dt = torch.empty((B, NQ, H, D), dtype=torch.float32, device="cuda")
         d = xq.DevTensor(wl.F32, (D, H, NQ, B), (4, D * 4, H * D * 4, NQ * H * D * 4), dt)
@@ -355,6 +358,38 @@ def main():
                          "bytes_per_launch": alg, "avg_launch_us": round(k_us, 3)},
             "kernels": kt,
         })
+
+    # ---------------- the other attention configs: f16 decode at 4k, q4_0 MTP verify
+    if args.only in ("fa", "all"):
+        for key, xcfg, comp in (("fa_decode_f16", wl.FA_C1, "f16 MFMA scores (f32 Q as f16 hi + lo) and values"),
+                                ("fa_verify", wl.FA_C5, "int8 MFMA q4_0 scores, f16 MFMA values")):
+            x_sets_n = max(2, math.ceil(512 * 2**20 / xcfg.kv_bytes()))
+            log(f"building {x_sets_n} input sets of {xcfg.name}")
+            xsets = make_fa_sets(torch, xq, wl, xcfg, x_sets_n, seed=3)
+            xp = xq.fa_params(xcfg.kq_scale)
+            xq0, xk0, xv0, xm0, xd0 = xsets[0]
+            xws = torch.empty(xq.flash_attn_ext_workspace(xq0, xk0, xv0, xm0, None, xd0, xp) + 256,
+                              dtype=torch.uint8, device="cuda")
+
+            def x_call(i, xsets=xsets, xp=xp, xws=xws):
+                q, k, v, m, d = xsets[i]
+                xq.flash_attn_ext(q, k, v, m, None, d, xp, workspace=xws)
+
+            x_ms, x_n = graph_time(torch, x_call, x_sets_n, args.steps, args.warmup)
+            xkt = kernel_times(torch, xq, x_call, x_sets_n, args.steps)
+            x_alg = xcfg.algorithmic_bytes()
+            x_kus = xkt.get("fa_dec", {}).get("avg_us", float("nan"))
+            out[key] = {"workload": xcfg.name, "kv_type": {wl.F16: "f16", wl.Q4_0: "q4_0"}[xcfg.kv_type],
+                        "n_q": xcfg.n_q, "n_seq": xcfg.B, "kv_len": xcfg.L, "compute": comp,
+                        "us_per_call": round(x_ms * 1000, 3), "algorithmic_bytes": x_alg,
+                        "call_GB/s": round(x_alg / (x_ms * 1e-3) / 1e9, 1),
+                        "fa_dec_avg_us": round(x_kus, 3),
+                        "fa_dec_GB/s": round(x_alg / (x_kus * 1e-6) / 1e9, 1),
+                        "fa_dec_frac": round(x_alg / (x_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
+                        "tokens_per_s_equiv": round(xcfg.B * xcfg.n_q / (x_ms * 1e-3), 1),
+                        "input_sets": x_sets_n, "timed_calls": x_n, "kernels": xkt}
+            log(f"{key}: {x_ms * 1000:.2f} us/call, fa_dec {x_kus:.2f} us")
+            del xsets, xws
 
     # ---------------- GDN decode step
     gcfg = wl.GDN_C3

@@ -153,10 +153,10 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
     const int li = threadIdx.x & 15;
     const int col0 = cblk * COLS + (int)(threadIdx.x >> 4);
 
-    // the first token's inputs, then the state in column order, so column j
-    // computes (and stores) as soon as its own state has arrived
-    StepIn<CPT> ia;
-    load_token<BF16, VEC, CPT>(a, b, h, kh, li, col0, 0, ia);
+    // the state first, in column order, then the first token's inputs
+    // (6.51-6.55 us per call at 8 sequences, against 6.55-6.59 us with the
+    // inputs first); column j computes and stores as soon as its own state
+    // has arrived
     const float* s_in = (const float*)((const char*)a.state + (int64_t)b * a.s_nb3) + (int64_t)h * 16384;
     float4 s0[CPT], s1[CPT];
 #pragma unroll
@@ -165,6 +165,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
         s0[j] = ld_state(sc + 4 * li);
         s1[j] = ld_state(sc + 64 + 4 * li);
     }
+    StepIn<CPT> ia;
+    load_token<BF16, VEC, CPT>(a, b, h, kh, li, col0, 0, ia);
     float* out = (float*)((char*)a.dst + (int64_t)b * a.dst_nb2);
     if constexpr (ONE) {
         step_token<CPT, true>(a, ia, s0, s1, out, h, li, col0, 0);
