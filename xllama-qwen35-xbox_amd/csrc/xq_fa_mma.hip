@@ -19,9 +19,11 @@
 //           q8_0 / q4_0 K: v_mfma_i32_16x16x32_i8 per 32-element block, the
 //           exact integer block dot of ggml's vec_dot_q8_0_q8_0 /
 //           vec_dot_q4_0_q8_0 between the K block and the q8_0-quantised Q
-//           row (q4_0 nibbles enter unsigned and 8*sum(q) is removed), then
-//           scaled by d_k * d_q (one 4-block v_mfma_f32_16x16x1f32 forms the
-//           products of four blocks in the score layout) in f32.
+//           row, then scaled by d_k * d_q (one 4-block v_mfma_f32_16x16x1f32
+//           forms the products of four blocks in the score layout) in f32.
+//           q4_0 nibbles n enter as the signed bytes 16*(n - 8) against
+//           d_q/16: the integer dot is 16x ggml's and the scale 1/16 of it,
+//           both exact, so every product, and so every score, is ggml's.
 //           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exact f16 K with Q
 //           split into f16 hi + lo parts (the NATIVE policy uses hi alone).
 //   values  O^T = V^T P^T through v_mfma_f32_16x16x16_f16, A = 16 head dims,
@@ -72,7 +74,7 @@ struct DecCfg {
     static constexpr int NB = D / kQK;                 // 32-element blocks per row
     static constexpr int NPP = 16 * MT;
     static constexpr bool QUANT = is_quant(KT);
-    static constexpr int QRB = QUANT ? D + 8 * NB : 0;      // LDS Q image row bytes (int8 path)
+    static constexpr int QRB = QUANT ? D + 8 * NB : 0;      // LDS Q image row bytes (int8 path; d_q then 4*NB spare bytes that keep the stride)
     static constexpr int RING_W = 2 * 2 * SLICE;            // per wave: 2 stages x (K, V)
     static constexpr int MASK_W = 2 * MT * 512;             // per wave: 2 stages x MT x 2 f16 pairs per lane
     static constexpr int FIXED = NPP * QRB + 2 * 8 * NPP * 4 + 64;
@@ -89,8 +91,9 @@ struct DecCfg {
 };
 
 // 8 K bytes (elements 8g..8g+7 of block b) of a q8_0 / q4_0 record in LDS as
-// an int8 MFMA operand. q4_0 gives unsigned nibbles: elements 0..15 are the
-// low nibbles of bytes 0..15, elements 16..31 the high nibbles.
+// an int8 MFMA operand. q4_0 elements 0..15 are the low nibbles of bytes
+// 0..15, elements 16..31 the high nibbles; nibble n becomes the signed byte
+// 16*(n - 8) = (n << 4) ^ 0x80.
 template <int KT>
 XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     constexpr int BB = KT == XQ_TYPE_Q8_0 ? 34 : 18;
@@ -106,9 +109,9 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
         w1 = __builtin_amdgcn_alignbyte(c, m, 2);
     }
     if constexpr (KT == XQ_TYPE_Q4_0) {
-        const int ns = (g >> 1) * 4;
-        w0 = (w0 >> ns) & 0x0f0f0f0fu;
-        w1 = (w1 >> ns) & 0x0f0f0f0fu;
+        const int ls = 4 - (g >> 1) * 4;  // low nibbles move to the high half of the byte
+        w0 = ((w0 << ls) & 0xf0f0f0f0u) ^ 0x80808080u;
+        w1 = ((w1 << ls) & 0xf0f0f0f0u) ^ 0x80808080u;
     }
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
@@ -411,29 +414,21 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             const float dblk = amax / 127.0f;
             const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
             uint32_t packed = 0;
-            int qsum = 0;
 #pragma unroll
             for (int j = 0; j < VD; ++j) {
                 const int qv = (int)rintf(x[k][j] * id);
                 packed |= (uint32_t)(uint8_t)(int8_t)qv << (8 * j);
-                qsum += qv;
             }
             if constexpr (VD == 4)
                 *(uint32_t*)(img + 4 * lane) = packed;
             else
                 *(uint16_t*)(img + 2 * lane) = (uint16_t)packed;
-            float qs = (float)qsum;  // exact: |sum| <= 32*127
-            qs += dpp<0xB1>(qs);
-            qs += dpp<0x4E>(qs);
-            qs += dpp<0x141>(qs);
-            if constexpr (LPB == 16) qs += dpp<0x140>(qs);
             if ((lane % LPB) == 0) {
                 const int blk = (lane * VD) / kQK;
                 const float dqv = f16_bits_to_f32(f32_to_f16_bits(dblk));
-                ((float*)(img + D))[blk] = dqv;
-                // q4_0: the dot with unsigned nibbles carries +8*sum(q); removed as the
-                // exact integer -8*sum(q) before the block scale applies
-                ((int*)(img + D + 4 * NB))[blk] = KT == XQ_TYPE_Q4_0 ? -8 * (int)qs : 0;
+                // q4_0 K bytes are 16x the signed nibbles: d_q / 16 (exact) keeps each
+                // product d_k * d_q * dot
+                ((float*)(img + D))[blk] = KT == XQ_TYPE_Q4_0 ? dqv * 0.0625f : dqv;
             }
         }
         if (t0 + step < r_end) {
@@ -477,9 +472,8 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // ---- B operands of the score product: pair 16m + lr, elements 8lg..8lg+7 of each block
     int64_t qb[QUANT ? MT : 1][QUANT ? NB : 1];
     // dqb[m][q]: d_q of block 4q + lg of the lane's pair (the B operand of the
-    // 4-block scale product); qci: the q4_0 correction -8*sum(q) per block
+    // 4-block scale product)
     float dqb[QUANT ? MT : 1][QUANT ? NB / 4 : 1];
-    int qci[KT == XQ_TYPE_Q4_0 ? MT : 1][KT == XQ_TYPE_Q4_0 ? NB : 1];
     if constexpr (QUANT) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -488,7 +482,6 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             for (int c = 0; c < NB; ++c) {
                 qb[m][c] = *(const int64_t*)(img + 32 * c + 8 * lg);
                 if (c % 4 == 0) dqb[m][c / 4] = ((const float*)(img + D))[c + lg];
-                if constexpr (KT == XQ_TYPE_Q4_0) qci[m][c] = ((const int*)(img + D + 4 * NB))[c];
             }
         }
     }
@@ -538,9 +531,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     for (int m = 0; m < MT; ++m)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            int iv = I[m][j][i];
-                            if constexpr (KT == XQ_TYPE_Q4_0) iv += qci[m][c0 + j];
-                            s[m][i] = fmaf((float)iv, dks[m][4 * j + i], s[m][i]);
+                            s[m][i] = fmaf((float)I[m][j][i], dks[m][4 * j + i], s[m][i]);
                         }
             }
         } else {
