@@ -437,6 +437,11 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             v_unit(t0 + step, 1);
         }
     } else {
+        // ring stage 0 first: its loads overlap the Q loads' round trip
+        if (t0 < r_end) {
+            k_unit(t0, 0);
+            v_unit(t0, 0);
+        }
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const int p = 16 * m + lr;
@@ -457,10 +462,6 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                                             : __builtin_bit_cast(_Float16, (uint16_t)f32_to_f16_bits(xv - f16_bits_to_f32(hb)));
                 }
             }
-        }
-        if (t0 < r_end) {
-            k_unit(t0, 0);
-            v_unit(t0, 0);
         }
         if (t0 + step < r_end) {
             k_unit(t0 + step, 1);
