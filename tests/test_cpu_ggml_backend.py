@@ -83,3 +83,33 @@ def test_supports_op_noop_and_other_kinds():
     assert not xqattn.ggml_supports_op(xqattn.GgmlNode(xqattn.OP_OTHER, dst))
     assert not xqattn.ggml_supports_op(xqattn.GgmlNode(7, dst))
     assert xqattn.load().xq_ggml_supports_op(None) == 0
+
+
+def test_c_header_layout_matches_ctypes(tmp_path):
+    """The C declarations of include/xq_ggml_backend.h, compiled by the host C
+    compiler, have the field offsets the ctypes mirror uses."""
+    import shutil
+    import subprocess
+    from conftest import ROOT
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    src = tmp_path / "layout.c"
+    src.write_text("""
+#include <stddef.h>
+#include <stdio.h>
+#include "xq_ggml_backend.h"
+int main(void) {
+    printf("%zu %zu %zu %zu %zu %zu %zu\\n", sizeof(xq_tensor), offsetof(xq_ggml_node, op_params),
+           offsetof(xq_ggml_node, dst), offsetof(xq_ggml_node, src), sizeof(xq_ggml_node),
+           sizeof(xq_ggml_backend_params), sizeof(xq_fa_params));
+    return 0;
+}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(xqattn.XqTensor), xqattn.XqGgmlNode.op_params.offset, xqattn.XqGgmlNode.dst.offset,
+            xqattn.XqGgmlNode.src.offset, ctypes.sizeof(xqattn.XqGgmlNode),
+            ctypes.sizeof(xqattn.XqGgmlBackendParams), ctypes.sizeof(xqattn.XqFaParams)]
+    assert got == want
