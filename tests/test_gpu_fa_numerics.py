@@ -1,0 +1,299 @@
+"""GPU numerics of GGML_OP_FLASH_ATTN_EXT beyond the N(0,1) configurations:
+
+* the value path's accuracy does not depend on V's magnitude (C2 / C5 geometry,
+  V scaled by 1e-1 .. 1e-3, both engines, bound relative to max|f64|);
+* KV dequantisation inside the kernels is bit-exact: with Q = 0 and one visible
+  row per (query, head) the output is that row's dequantised V, bit for bit
+  (shaders/rkva/rkva_range_attn.hlsl:28-57 decoders, ggml's to_float);
+* rows a query does not see never reach it, even when they hold Inf/NaN, and a
+  range call turns exactly the rows that see a non-finite record into NaN
+  (shaders/rkva/rkva_range_reduce_opt.hlsl:39-56,126-132);
+* a query's bits do not depend on how many queries (n_q 1 / 3 / 8) or, under
+  the length-only split modes, how many sequences (B 1 / 4) share the call, at
+  the 32k head-dim-256 geometry (patches/0008-flash-attn-query-consistency.patch:40-56,
+  uwp/rkva/rkva-range-profile.h:99-107);
+* the verify configuration at full size with padded and fully masked query rows.
+"""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle
+import xqattn
+from conftest import assert_close, case_note
+from fa_cases import make_fa_case, oracle_f64, oracle_fa, run_fa_gpu
+from xqattn import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+ENGINES = [xqattn.ENGINE_MFMA, xqattn.ENGINE_VALU]
+ENGINE_IDS = ["mfma", "valu"]
+NAN16, INF16 = 0x7E00, 0x7C00
+
+
+# ---------------------------------------------------------------------------
+# value path vs V's magnitude
+# ---------------------------------------------------------------------------
+
+_VCACHE = {}
+
+
+def _vscale_case(cfg, v_scale):
+    key = (cfg.name, v_scale)
+    if key not in _VCACHE:
+        _VCACHE.clear()  # one full-size case in memory at a time
+        case = make_fa_case(cfg, seed=11, v_scale=v_scale)
+        ref, _ = oracle_f64(case)
+        _VCACHE[key] = (case, ref)
+    return _VCACHE[key]
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("v_scale", [1e-1, 1e-2, 1e-3])
+@pytest.mark.parametrize("cfg", [wl.FA_C2, wl.FA_C5], ids=lambda c: c.name)
+def test_fa_value_path_independent_of_v_scale(torch_gpu, cfg, v_scale, engine):
+    """max|gpu - f64| / max|f64| <= 1e-3 whatever V's scale: the weight x block
+    scale products keep f32's exponent range on both engines."""
+    case_note(f"v_scale {v_scale} {cfg.name} engine {engine}")
+    case, ref = _vscale_case(cfg, v_scale)
+    got, _ = run_fa_gpu(case, torch_gpu, engine=engine)
+    rel = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+    print(f"{cfg.name} v_scale {v_scale} engine {engine}: max|gpu-f64|/max|f64| = {rel:.2e}")
+    assert rel <= 1e-3, rel
+
+
+# ---------------------------------------------------------------------------
+# dequantisation bit-exact
+# ---------------------------------------------------------------------------
+
+def _one_row_case(kv_type, D, seed=3):
+    B, NQ, H, Hkv, L = 1, 4, 8, 2, 300
+    G = H // Hkv
+    cfg = wl.FaConfig("one_row", NQ, H, Hkv, D, L, B, kv_type)
+    vf = wl.normal(seed, (B, L, Hkv, D)) * np.float32(3.0)
+    vf[0, 7, 0, :] = np.float32(1e-6)   # tiny values (f16 subnormal records)
+    vraw = oracle.quantize(kv_type, vf)
+    kraw = oracle.quantize(kv_type, wl.normal(seed + 1, (B, L, Hkv, D)))
+    q = np.zeros((B, NQ, H, D), np.float32)
+    rows = np.array([[(37 * iq + 101 * h + 13) % L for h in range(H)] for iq in range(NQ)])
+    rows[0, 0] = 7
+    m = np.full((1, H, NQ, L), 0xFC00, np.uint16)  # [Bm, H, n_q, L]: per-head mask planes
+    for iq in range(NQ):
+        for h in range(H):
+            m[0, h, iq, rows[iq, h]] = 0
+    mask = wl.HostTensor(wl.F16, (L, NQ, H, 1), (2, 2 * L, 2 * L * NQ, 2 * L * NQ * H), m.reshape(-1).view(np.uint8))
+    case = dataclasses.replace(
+        make_fa_case(cfg, seed=seed, mask=None), q=wl.fa_q_tensor(q), k=wl.kv_tensor(kraw, kv_type, D),
+        v=wl.kv_tensor(vraw, kv_type, D), mask=mask)
+    deq = oracle.dequant(kv_type, vraw, D)  # [B, L, Hkv, D]
+    want = np.empty((B, NQ, H, D), np.float32)
+    for iq in range(NQ):
+        for h in range(H):
+            want[0, iq, h] = deq[0, rows[iq, h], h // G]
+    return case, want
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("split_mode", [xqattn.SPLIT_AUTO, xqattn.SPLIT_NONE], ids=["auto", "none"])
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2], ids=lambda t: wl.TYPE_NAME[t])
+def test_fa_dequant_bit_exact_one_visible_row(torch_gpu, kv_type, D, split_mode, engine):
+    """Q = 0 and one visible row per (query, head): every weight is a power of two
+    and the output is the dequantised V row, bit for bit."""
+    case_note(f"one visible row {wl.TYPE_NAME[kv_type]} D{D} split {split_mode} engine {engine}")
+    case, want = _one_row_case(kv_type, D)
+    got, lse = run_fa_gpu(case, torch_gpu, split_mode=split_mode, engine=engine)
+    # equal as floats: every nonzero element bit for bit; a zero element may
+    # carry either sign (ggml's accumulator also starts at +0, so 0*d with d < 0
+    # leaves +0 in its output too)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} elements differ, first {bad[0]}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+    nz = want != 0
+    assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+    assert np.all(np.abs(lse) < 1e-6)
+
+
+# ---------------------------------------------------------------------------
+# non-finite records
+# ---------------------------------------------------------------------------
+
+def _spoil(raw, kv_type, row, head, what):
+    """Make one record of raw [L, Hkv, rec] non-finite: an element (F16, E5M2) or
+    the scale of block 1 (q8_0, q4_0)."""
+    rec = raw[row, head]
+    if kv_type == wl.F16:
+        rec[10:12] = np.frombuffer(np.uint16(NAN16 if what == "nan" else INF16).tobytes(), np.uint8)
+    elif kv_type == wl.E5M2:
+        rec[5] = 0x7F if what == "nan" else 0x7C
+    else:
+        bb = 34 if kv_type == wl.Q8_0 else 18
+        rec[bb:bb + 2] = np.frombuffer(np.uint16(NAN16 if what == "nan" else INF16).tobytes(), np.uint8)
+
+
+@pytest.mark.parametrize("split_mode", [xqattn.SPLIT_NONE, xqattn.SPLIT_REFERENCE], ids=["one_split", "splits"])
+@pytest.mark.parametrize("where,what", [("k", "nan"), ("v", "nan"), ("v", "inf")])
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2], ids=lambda t: wl.TYPE_NAME[t])
+def test_fa_range_nonfinite_record_poisons_exactly_the_rows_that_see_it(torch_gpu, kv_type, where, what,
+                                                                        split_mode):
+    """A NaN/Inf K or V record at row R of KV head 1 makes OUT and LSE NaN for
+    exactly the (query, head) rows with head in KV head 1's group whose causal
+    limit passes R; every other row stays finite and matches the oracle."""
+    torch = torch_gpu
+    n_head, hkv, D, origin, active, R = 8, 2, 128, 1000, 700, 400
+    G = n_head // hkv
+    kraw = oracle.quantize(kv_type, wl.normal(81, (active, hkv, D)))
+    vraw = oracle.quantize(kv_type, wl.normal(82, (active, hkv, D)))
+    _spoil(kraw if where == "k" else vraw, kv_type, R, 1, what)
+    positions = np.array([origin + 300, origin + R, origin + R - 1, origin + 699, origin - 3, origin + 2000],
+                         np.int32)
+    n_q = positions.size
+    q = wl.normal(83, (n_q, n_head, D))
+    scale = 1.0 / 16
+    limit = np.minimum(active, np.maximum(positions - origin + 1, 0))
+    want_nan = np.zeros((n_q, n_head), bool)
+    for i in range(n_q):
+        for h in range(n_head):
+            want_nan[i, h] = h // G == 1 and limit[i] > R
+    split_k = xqattn.split_count(active, split_mode)
+    want, wlse, _ = oracle.range_attn(q, positions, n_head, kraw, vraw, hkv, D, kv_type, origin, active, scale,
+                                      split_k)
+    assert np.array_equal(np.isnan(wlse), want_nan), "oracle poisoning pattern"
+    case_note(f"range non-finite {wl.TYPE_NAME[kv_type]} {where} {what} split {split_mode}")
+    out = torch.empty(n_q * n_head * D, dtype=torch.float32, device="cuda")
+    lse = torch.empty(n_q * n_head, dtype=torch.float32, device="cuda")
+    xqattn.fa_range(torch.from_numpy(q).cuda(), torch.from_numpy(positions).cuda(), n_head,
+                    torch.from_numpy(kraw.reshape(-1)).cuda(), torch.from_numpy(vraw.reshape(-1)).cuda(),
+                    hkv, D, kv_type, origin, active, scale, out, lse, split_mode=split_mode)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(n_q, n_head, D)
+    glse = lse.cpu().numpy().reshape(n_q, n_head)
+    assert np.array_equal(np.isnan(glse), want_nan), f"LSE NaN rows {np.argwhere(np.isnan(glse))}"
+    assert np.all(np.isnan(got[want_nan])), "a row that sees the record is not NaN in full"
+    assert np.all(np.isfinite(got[~want_nan])), "a row that does not see the record is not finite"
+    assert_close(got[~want_nan], want[~want_nan], atol=3e-4, rtol=3e-4, what="finite rows O")
+    assert_close(glse[~want_nan], wlse[~want_nan], atol=3e-4, rtol=3e-5, what="finite rows LSE")
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2], ids=lambda t: wl.TYPE_NAME[t])
+def test_fa_masked_nonfinite_rows_never_reach_a_query(torch_gpu, kv_type, engine):
+    """ggml's loop skips masked rows: NaN K/V records in rows masked for every
+    query change nothing (bitwise); a NaN V record in a row only query 2 sees
+    makes query 2's rows of that KV head non-finite and leaves queries 0, 1
+    bitwise unchanged."""
+    cfg = wl.FaConfig("masknan", 3, 16, 4, 128, 500, 2, kv_type, causal_prefix=400)
+    case_note(f"masked non-finite rows {wl.TYPE_NAME[kv_type]} engine {engine}")
+    case = make_fa_case(cfg, seed=61, mask_per_seq=True)
+    clean, clse = run_fa_gpu(case, torch_gpu, engine=engine)
+    rec = wl.record_bytes(kv_type, 128)
+    k = case.k.buf.reshape(2, 500, 4, rec).copy()
+    v = case.v.buf.reshape(2, 500, 4, rec).copy()
+    for r in range(450, 461):
+        for h in range(4):
+            _spoil(k[0], kv_type, r, h, "nan")
+            _spoil(v[1], kv_type, r, h, "nan")
+    spoiled = dataclasses.replace(case, k=wl.kv_tensor(k, kv_type, 128), v=wl.kv_tensor(v, kv_type, 128))
+    got, glse = run_fa_gpu(spoiled, torch_gpu, engine=engine)
+    assert np.array_equal(got, clean) and np.array_equal(glse, clse), "masked non-finite rows changed the output"
+    # row 402 is visible to query 2 only (query i sees rows <= 400 + i)
+    v2 = v.copy()
+    _spoil(v2[0], kv_type, 402, 1, "nan")
+    spoiled2 = dataclasses.replace(spoiled, v=wl.kv_tensor(v2, kv_type, 128))
+    got2, _ = run_fa_gpu(spoiled2, torch_gpu, engine=engine)
+    heads1 = slice(4, 8)  # query heads of KV head 1 (GQA 4)
+    assert np.array_equal(got2[:, :2], clean[:, :2]), "queries 0, 1 do not see row 402"
+    assert np.array_equal(got2[1], clean[1]), "sequence 1 does not read sequence 0's cache"
+    assert not np.all(np.isfinite(got2[0, 2, heads1])), "query 2 sees the NaN row"
+    assert np.array_equal(got2[0, 2, :4], clean[0, 2, :4]) and np.array_equal(got2[0, 2, 8:], clean[0, 2, 8:])
+
+
+# ---------------------------------------------------------------------------
+# batch-composition invariance at the 32k, head-dim-256 geometry
+# ---------------------------------------------------------------------------
+
+_CASES = {}
+
+
+def _cached_case(cfg, **kw):
+    key = (cfg, tuple(sorted(kw.items())))
+    if key not in _CASES:
+        _CASES.clear()  # one full-size case in memory at a time
+        _CASES[key] = make_fa_case(cfg, **kw)
+    return _CASES[key]
+
+
+def _sub_case(case, iq0, n, b_sel=None):
+    """The same K/V with queries [iq0, iq0 + n) (and sequences b_sel) only."""
+    B, NQ, H, D = case.shape
+    L = case.cfg.L
+    q_all = np.frombuffer(case.q.buf.tobytes(), np.float32).reshape(B, NQ, H, D)
+    m_all = np.frombuffer(case.mask.buf.tobytes(), np.uint16).reshape(case.mask.ne[3], case.mask.ne[1], L)
+    kv = case.k, case.v
+    if b_sel is not None:
+        if m_all.shape[0] == B:
+            m_all = m_all[b_sel]
+        rec = wl.record_bytes(case.cfg.kv_type, D)
+        kv = tuple(wl.kv_tensor(t.buf.reshape(B, L, case.cfg.Hkv, rec)[b_sel].copy(), case.cfg.kv_type, D)
+                   for t in kv)
+        q_all = q_all[b_sel]
+        B = q_all.shape[0]
+    cfg = dataclasses.replace(case.cfg, n_q=n, B=B)
+    return dataclasses.replace(case, cfg=cfg, q=wl.fa_q_tensor(q_all[:, iq0:iq0 + n].copy()),
+                               k=kv[0], v=kv[1], mask=wl.mask_tensor(m_all[:, iq0:iq0 + n].copy()),
+                               dst=wl.fa_dst_tensor(B, n, H, D))
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("kv_type", [wl.Q8_0, wl.Q4_0, wl.E5M2], ids=lambda t: wl.TYPE_NAME[t])
+def test_fa_query_width_invariance_c2_geometry(torch_gpu, kv_type, engine):
+    """n_q = 1, 3 and 8 give the same bits for a query at L = 32768, D = 256,
+    GQA 6, B = 4 (2048-row splits: many 16-row slices per wave)."""
+    cfg = wl.FaConfig("inv_c2", 8, 24, 4, 256, 32768, 4, kv_type, causal_prefix=32760)
+    case_note(f"query width invariance C2 geometry {wl.TYPE_NAME[kv_type]} engine {engine}")
+    case = _cached_case(cfg, seed=5)
+    batch, blse = run_fa_gpu(case, torch_gpu, engine=engine)
+    for iq0, n in ((0, 1), (3, 1), (7, 1), (2, 3), (5, 3)):
+        sub, slse = run_fa_gpu(_sub_case(case, iq0, n), torch_gpu, engine=engine)
+        assert np.array_equal(sub, batch[:, iq0:iq0 + n]), f"queries {iq0}..{iq0 + n - 1} differ at n_q={n}"
+        assert np.array_equal(slse, blse[:, iq0:iq0 + n])
+
+
+@pytest.mark.parametrize("split_mode", [xqattn.SPLIT_REFERENCE, xqattn.SPLIT_BALANCED, xqattn.SPLIT_COARSE],
+                         ids=["reference", "balanced", "coarse"])
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+def test_fa_sequence_batch_invariance_length_only_split_modes(torch_gpu, engine, split_mode):
+    """Under split modes that depend on the KV length only, a sequence's output
+    is bitwise the same alone (B = 1) or in a batch of four (B = 4)."""
+    cfg = wl.FaConfig("inv_b", 2, 24, 4, 256, 32768, 4, wl.Q8_0, causal_prefix=32766)
+    case_note(f"sequence batch invariance split {split_mode} engine {engine}")
+    case = _cached_case(cfg, seed=8, mask_per_seq=True)
+    batch, blse = run_fa_gpu(case, torch_gpu, split_mode=split_mode, engine=engine)
+    for b in (0, 2):
+        alone, alse = run_fa_gpu(_sub_case(case, 0, 2, b_sel=slice(b, b + 1)), torch_gpu, split_mode=split_mode,
+                                 engine=engine)
+        assert np.array_equal(alone[0], batch[b]), f"sequence {b} differs between B=1 and B=4"
+        assert np.array_equal(alse[0], blse[b])
+
+
+# ---------------------------------------------------------------------------
+# the verify configuration with padded and fully masked query rows
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+def test_fa_verify_full_size_masked_query_rows(torch_gpu, engine):
+    """C5 at full size (n_q 8, L 16392, q4_0, B 8) with the mask padded to 16
+    rows and queries 6 and 7 fully masked (-inf rows): those give O = 0 and
+    LSE = -inf, the others match the oracle."""
+    cfg = dataclasses.replace(wl.FA_C5, name="c5_masked_rows", n_q_pad=16)
+    case_note(f"C5 full size masked query rows engine {engine}")
+    case = make_fa_case(cfg, seed=12)
+    m = wl.fa_causal_mask(cfg, n_q_rows=6)  # rows 6..15 all -inf
+    case.mask = wl.mask_tensor(m)
+    got, glse = run_fa_gpu(case, torch_gpu, engine=engine)
+    assert np.all(got[:, 6:] == 0.0) and np.all(np.isneginf(glse[:, 6:]))
+    want, wlse = oracle_fa(case)
+    assert_close(got, want, what="C5 masked query rows vs ggml restatement")
+    ref64, lse64 = oracle_f64(case)
+    assert_close(got[:, :6], ref64[:, :6], atol=1e-4, rtol=1e-4, what="C5 vs f64")
+    assert_close(glse[:, :6], lse64[:, :6], atol=1e-4, rtol=1e-5, what="C5 LSE")

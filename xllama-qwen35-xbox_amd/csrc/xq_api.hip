@@ -196,7 +196,7 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
     P.q_round_f16 = (p->qk_policy == XQ_FA_QK_NATIVE && k->type == XQ_TYPE_F16) ? 1 : 0;
     split_policy(P.L, p->split_mode, B * Hkv, &P.n_splits, &P.split_rows);
     if (P.n_splits > 256) return fail(XQ_ERR_UNSUPPORTED, "more than 256 KV splits");
-    const int npairs = P.G * (P.NQ < 32 / P.G ? P.NQ : 32 / P.G);
+    const int npairs = P.G * xq::fa_query_tile(P.D, P.G, P.NQ);
     if (!xq::fa_kernel_available(P.kt, P.D, P.qk_mode, npairs))
         return fail(XQ_ERR_UNSUPPORTED, "no kernel for this combination");
     if (p->engine == XQ_FA_ENGINE_MFMA && !xq::fa_mma_available(P.kt, P.D, P.qk_mode, npairs))

@@ -154,6 +154,7 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
     __shared__ __attribute__((aligned(16))) float sP[kTile * PS];
     __shared__ float sAlpha[NP];
     __shared__ float sFin[NP][2];
+    __shared__ int sBad[NP];
 
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     uint32_t wg = xcd_remap(blockIdx.x, n_wg);
@@ -353,7 +354,13 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
             }
         }
 
-        // ---- online softmax per owned pair (ggml order: scale, softcap, + mask)
+        // ---- online softmax per owned pair (ggml order: scale, softcap, + mask).
+        //      A row the pair does not see (masked, past its limit or the tile)
+        //      gets the weight -0, a visible row whose weight underflows +0:
+        //      a tile with unseen rows is "careful", and there a non-finite V
+        //      element reaches only the pairs whose weight is not -0 (ggml's
+        //      loop never visits the rows it skips)
+        bool unseen = false;
 #pragma unroll
         for (int u = 0; u < UPW; ++u) {
             const int p = wave + 4 * u;
@@ -367,17 +374,18 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
                     s = s + mv;
                 }
                 s = valid ? s : -INFINITY;
+                unseen |= !valid;
                 const float tmax = wave_max(s);
                 const float m_new = fmaxf(m_run[u], tmax);
                 const float alpha = m_new == -INFINITY ? 1.0f : fast_exp(m_run[u] - m_new);
-                const float pr = s == -INFINITY ? 0.0f : fast_exp(s - m_new);
+                const float pr = s == -INFINITY ? -0.0f : fast_exp(s - m_new);
                 l_run[u] = fmaf(l_run[u], alpha, wave_sum(pr));
                 m_run[u] = m_new;
                 sP[lane * PS + p] = pr;
                 if (lane == 0) sAlpha[p] = alpha;
             }
         }
-        __syncthreads();
+        const bool careful = __syncthreads_or(unseen);
 
         // ---- values: wave owns dims [wave*D/4, (wave+1)*D/4), row group rg owns rows rg + 4i
 #pragma unroll
@@ -396,15 +404,36 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
             float vv[VD];
             decode_v<KT, VD>(sV + r * RECP, d0, vv);
             const float* pr = sP + r * PS;
+            bool vbad = false;
+            if (careful) {
 #pragma unroll
-            for (int p4 = 0; p4 < NP / 4; ++p4) {
-                if (4 * p4 < npa) {
-                    const float4 w4 = *(const float4*)(pr + 4 * p4);
-                    const float ws[4] = {w4.x, w4.y, w4.z, w4.w};
+                for (int j = 0; j < VD; ++j) vbad |= !__builtin_isfinite(vv[j]);
+            }
+            if (vbad) {
 #pragma unroll
-                    for (int t = 0; t < 4; ++t)
+                for (int p4 = 0; p4 < NP / 4; ++p4) {
+                    if (4 * p4 < npa) {
+                        const float4 w4 = *(const float4*)(pr + 4 * p4);
+                        const float ws[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-                        for (int j = 0; j < VD; ++j) acc[4 * p4 + t][j] = fmaf(ws[t], vv[j], acc[4 * p4 + t][j]);
+                        for (int t = 0; t < 4; ++t) {
+                            if (__float_as_uint(ws[t]) == 0x80000000u) continue;  // row unseen by the pair
+#pragma unroll
+                            for (int j = 0; j < VD; ++j) acc[4 * p4 + t][j] = fmaf(ws[t], vv[j], acc[4 * p4 + t][j]);
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int p4 = 0; p4 < NP / 4; ++p4) {
+                    if (4 * p4 < npa) {
+                        const float4 w4 = *(const float4*)(pr + 4 * p4);
+                        const float ws[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                        for (int t = 0; t < 4; ++t)
+#pragma unroll
+                            for (int j = 0; j < VD; ++j) acc[4 * p4 + t][j] = fmaf(ws[t], vv[j], acc[4 * p4 + t][j]);
+                    }
                 }
             }
         }
@@ -438,11 +467,42 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
                 if (lane == 0) {
                     sFin[p][0] = a1;
                     sFin[p][1] = inv;
-                    if (a.lse) a.lse[(int64_t)b * rows_per_seq + (int64_t)iq * a.H + h] = l;
+                    // the split reducer's rule with one split (range calls): a
+                    // non-finite or negative sum, factor or normaliser poisons the row
+                    const float S = l_run[u];
+                    sBad[p] = a.poison && (!__builtin_isfinite(S) || S < 0.0f || !__builtin_isfinite(inv) ||
+                                           (S != 0.0f && !__builtin_isfinite(l)));
+                    if (a.lse && !a.poison) a.lse[(int64_t)b * rows_per_seq + (int64_t)iq * a.H + h] = l;
                 }
             }
         }
         __syncthreads();
+        if (a.poison) {
+            // ... and so does a non-finite output element
+            if (rg == 0) {
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    if (p < npa) {
+                        const float a1 = sFin[p][0], inv = sFin[p][1];
+                        bool bad = false;
+#pragma unroll
+                        for (int j = 0; j < VD; ++j) bad |= !__builtin_isfinite((acc[p][j] * a1) * inv);
+                        if (bad) sBad[p] = 1;
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < UPW; ++u) {
+                const int p = wave + 4 * u;
+                if (p < npa && lane == 0 && a.lse) {
+                    const int qq = p / a.G, h = g * a.G + p % a.G, iq = iq0 + qq;
+                    float a1, inv, l;
+                    fa_finalize(m_run[u], l_run[u], a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, l);
+                    a.lse[(int64_t)b * rows_per_seq + (int64_t)iq * a.H + h] = sBad[p] ? NAN : l;
+                }
+            }
+        }
         if (rg == 0) {
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
@@ -450,8 +510,9 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
                     const int qq = p / a.G, h = g * a.G + p % a.G, iq = iq0 + qq;
                     float* o = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1) + d0;
                     const float a1 = sFin[p][0], inv = sFin[p][1];
+                    const bool bad = a.poison && sBad[p];
 #pragma unroll
-                    for (int j = 0; j < VD; ++j) o[j] = (acc[p][j] * a1) * inv;
+                    for (int j = 0; j < VD; ++j) o[j] = bad ? NAN : (acc[p][j] * a1) * inv;
                 }
             }
         }
@@ -878,9 +939,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
     }
     a.poison = L.poison;
 
-    const int max_pairs = 32;
-    int QT = G >= max_pairs ? 1 : max_pairs / G;
-    if (QT > NQ) QT = NQ;
+    int QT = fa_query_tile(D, G, NQ);
     if (QT < 1) QT = 1;
     a.QT = QT;
     a.n_qtiles = (NQ + QT - 1) / QT;

@@ -26,20 +26,37 @@
 //           both exact, so every product, and so every score, is ggml's.
 //           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exact f16 K with Q
 //           split into f16 hi + lo parts (the NATIVE policy uses hi alone).
-//   values  O^T = V^T P^T through v_mfma_f32_16x16x16_f16, A = 16 head dims,
-//           B = the weights of 16 pairs over four rows per lane. The score
-//           tile's output registers (lane = pair, four consecutive rows) are
-//           exactly the B operand layout of this product, so the softmax
-//           weights never leave registers and every per-pair quantity
-//           (maximum, sum, rescale factor) is lane-local. V is gathered from
-//           LDS per (row, dim) and converted exactly (int8 by SDWA sign-
-//           extending f16 conversions, q4_0 nibbles through the 0x6400
-//           exponent trick, E5M2 by a byte shift); the V block scale
-//           multiplies the weights in f16.
+//   values  O^T = V^T W^T over 32 products per MFMA, A = 16 head dims,
+//           B = the weights of 16 pairs. The score tile's output registers
+//           (lane = pair, four consecutive rows) hold exactly the rows a lane
+//           gives the B operand, so the softmax weights never leave registers
+//           and every per-pair quantity (maximum, sum, rescale factor) is
+//           lane-local. Each weight enters as a high and a low part (products
+//           8lg..8lg+3 of a lane group: its four rows' high parts, 8lg+4..
+//           8lg+7: their low parts; the V operand repeats the four rows), so
+//           the product carries ~22 (f16) or ~16 (bf16) significant bits of
+//           every weight:
+//           q8_0 / q4_0 V: v_mfma_f32_16x16x32_bf16 on the exact integer
+//           values (bf16 holds every int8) against w * d_v formed in f32 and
+//           split into bf16 high (truncated) + low (rounded) parts; bf16 has
+//           f32's exponent range, so the value path is exact in range for any
+//           block scale (an f16 product w * d_v falls into subnormals, and
+//           then to zero, as V's magnitude shrinks);
+//           F16 / E5M2 V: v_mfma_f32_16x16x32_f16 on the exact f16 V against
+//           the weight in f16 high + low parts (the weights lie in (0, 16]).
 // Online softmax in base 2 (scores pre-multiplied by log2 e) with a lazy
 // maximum: the running maximum moves only when a slice exceeds it by more
 // than 8, so accumulator rescales are rare; weights are taken relative to the
 // maximum plus 4 and so stay in (0, 16].
+//
+// Rows a pair does not see (mask -inf, past its causal limit or the split)
+// never touch its state, as ggml's loop skips them: a slice that holds such a
+// row or a non-finite score runs "careful" — the scores of unseen rows become
+// -inf whatever K holds, quantized V weights of unseen rows are zeroed before
+// the scale multiplies them, and non-finite F16/E5M2 V elements are replaced
+// by 0 in the shared V operand while every pair that sees such a row gets a
+// NaN state. Range calls (positions) additionally turn a row whose output or
+// normaliser is not finite into NaN in full (the split reducer's poisoning).
 #include <type_traits>
 
 #include "xq_fa_common.h"
@@ -49,6 +66,8 @@ namespace xq {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -116,25 +135,32 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
 
-// V^T operands of one q8_0 block: the signed bytes 0 (tile 0) and 1 (tile 1)
-// of the rows' 16-bit words x0..x3 as f16 pairs (rows 0,1 and rows 2,3),
-// exact. Each pair is two SDWA conversions of sign-extended bytes, the second
-// writing the high half and keeping the low one. The trailing s_nop gives the
-// two wait states an MFMA reading a VGPR needs after a VALU wrote it (the
-// compiler's hazard tracking does not see into the asm).
-XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32_t (&A0)[2], uint32_t (&A1)[2]) {
-    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %1, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
-        "v_cvt_f16_i16_sdwa %3, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
-        "v_cvt_f16_i16_sdwa %3, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
-        "s_nop 1"
-        : "=&v"(A0[0]), "=&v"(A0[1]), "=&v"(A1[0]), "=&v"(A1[1])
-        : "v"(x0), "v"(x1), "v"(x2), "v"(x3));
+// The signed bytes 0 and 1 of x as f32 (exact), two SDWA sign-extending
+// conversions (the compiler shifts before converting byte 1). The results feed
+// VALU instructions only, so no MFMA hazard hides in the asm.
+XQ_DEV void q8_pair_f32(uint32_t x, float& b0, float& b1) {
+    asm("v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=&v"(b0), "=v"(b1)
+        : "v"(x));
 }
+
+// bf16 bits of two f32 values whose low 16 bits are zero (exact), packed
+// (a in the low half).
+XQ_DEV uint32_t hi16_pair(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+// Halves of w (a pair of f16) that are Inf or NaN (all-ones exponent) set to 0.
+XQ_DEV uint32_t f16x2_zero_nonfinite(uint32_t w) {
+    const uint32_t t = ((w & 0x7c007c00u) + 0x04000400u) & 0x80008000u;  // 0x8000 per non-finite half
+    return w & ~((t >> 15) * 0xffffu);
+}
+
+// Nonzero when any f16 half of w is Inf or NaN.
+XQ_DEV uint32_t f16x2_nonfinite(uint32_t w) { return ((w & 0x7c007c00u) + 0x04000400u) & 0x80008000u; }
+// Nonzero when any E5M2 byte of w is Inf or NaN.
+XQ_DEV uint32_t e5m2x4_nonfinite(uint32_t w) { return ((w & 0x7c7c7c7cu) + 0x04040404u) & 0x80808080u; }
 
 // Reductions over the four 16-lane rows (lanes l, l^16, l^32, l^48) by
 // permlane swaps; every lane gets the same bits ((r0 op r2) op (r1 op r3)).
@@ -564,29 +590,17 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     };
 
     // ---- values of the slice in ring stage ST, block c:
-    //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x P^T
-    auto values = [&](auto st_tag, int c, const h2 (&P)[MT][2]) {
+    //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x W^T, the 32
+    //      products of a lane group being its four rows' weight high parts, then
+    //      their low parts (the V operand repeats the four rows)
+    //      pw: f32 weights (row 4lg + i, pair 16m + lr); xs: their scores (-inf
+    //      for rows the pair does not see); Bf: F16/E5M2 weight operands;
+    //      careful / vsan: the slice's careful mode and V sanitising
+    auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], const float (&xs)[MT][4], bool careful,
+                      const h8 (&Bf)[MT], bool vsan) {
         constexpr int ST = decltype(st_tag)::value;
         const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
-        h4 Bv[MT];
-        if constexpr (QUANT) {
-            uint32_t dvw[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
-            const uint32_t sel = ((BB * c) & 2) ? 0x07060302u : 0x05040100u;
-            const h2 d01 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[1], dvw[0], sel));
-            const h2 d23 = __builtin_bit_cast(h2, __builtin_amdgcn_perm(dvw[3], dvw[2], sel));
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                const h2 u = P[m][0] * d01, w = P[m][1] * d23;
-                Bv[m] = h4{u[0], u[1], w[0], w[1]};
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < MT; ++m) Bv[m] = h4{P[m][0][0], P[m][0][1], P[m][1][0], P[m][1][1]};
-        }
-        // V^T operands of tiles t = 0, 1: f16 pairs of rows (0,1), (2,3)
-        uint32_t X[4], A0[2], A1[2];
+        uint32_t X[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const uint8_t* vr = Vs + (4 * lg + e) * REC;
@@ -599,34 +613,76 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             else
                 X[e] = lds_u16(vr + 32 * c + 2 * lr);
         }
-        if constexpr (KT == XQ_TYPE_Q8_0) {
-            q8_vt_f16(X[0], X[1], X[2], X[3], A0, A1);
+        if constexpr (QUANT) {
+            // d_v of rows 4lg + i, block c, in f32 (exact)
+            float dv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
+                dv[i] = f16_bits_to_f32(((BB * c) & 2) ? w >> 16 : w & 0xffffu);
+            }
+            // B: w * d_v in f32, split into bf16 high (truncated, exact) and
+            // low (the exact remainder rounded to bf16) parts
+            bf8 Bq[MT];
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                float xv[4], lo[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    xv[i] = pw[m][i] * dv[i];
+                    if (careful) xv[i] = xs[m][i] == -INFINITY ? 0.0f : xv[i];  // unseen rows add nothing, whatever d_v is
+                    lo[i] = xv[i] - __uint_as_float(__float_as_uint(xv[i]) & 0xffff0000u);
+                }
+                const bf2 l01 = {(__bf16)lo[0], (__bf16)lo[1]}, l23 = {(__bf16)lo[2], (__bf16)lo[3]};
+                Bq[m] = __builtin_bit_cast(bf8, uint4{hi16_pair(xv[0], xv[1]), hi16_pair(xv[2], xv[3]),
+                                                      __builtin_bit_cast(uint32_t, l01),
+                                                      __builtin_bit_cast(uint32_t, l23)});
+            }
+            // A: the integer values of tile t's dims in rows 4lg..4lg+3 as bf16 (exact)
+            float f0[4], f1[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (KT == XQ_TYPE_Q8_0) {
+                    q8_pair_f32(X[e], f0[e], f1[e]);
+                } else {  // q4_0: low nibble (dim lr of the block), high nibble (dim 16 + lr)
+                    f0[e] = (float)((int)(X[e] & 15u) - 8);
+                    f1[e] = (float)((int)(X[e] >> 4) - 8);
+                }
+            }
+            const uint32_t a01 = hi16_pair(f0[0], f0[1]), a23 = hi16_pair(f0[2], f0[3]);
+            const uint32_t b01 = hi16_pair(f1[0], f1[1]), b23 = hi16_pair(f1[2], f1[3]);
+            const bf8 At0 = __builtin_bit_cast(bf8, uint4{a01, a23, a01, a23});
+            const bf8 At1 = __builtin_bit_cast(bf8, uint4{b01, b23, b01, b23});
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(At0, Bq[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(At1, Bq[m], acc[m][2 * c + 1], 0, 0, 0);
+            }
         } else {
+            // A: f16 pairs of rows (0,1), (2,3) of tiles t = 0, 1 (exact)
+            uint32_t A0[2], A1[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const uint32_t x0 = X[2 * e], x1 = X[2 * e + 1];
-                if constexpr (KT == XQ_TYPE_Q4_0) {
-                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
-                    const uint32_t w = x0 | (x1 << 16);
-                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
-                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
-                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
-                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
-                } else if constexpr (KT == XQ_TYPE_F16) {
+                if constexpr (KT == XQ_TYPE_F16) {
                     A0[e] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
                     A1[e] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-                } else {
+                } else {  // E5M2: byte b -> f16 bits b << 8
                     A0[e] = __builtin_amdgcn_perm(x1, x0, 0x040c000cu);
                     A1[e] = __builtin_amdgcn_perm(x1, x0, 0x050c010cu);
                 }
+                if (vsan) {
+                    A0[e] = f16x2_zero_nonfinite(A0[e]);
+                    A1[e] = f16x2_zero_nonfinite(A1[e]);
+                }
             }
-        }
-        const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
-        const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
+            const h8 At0 = __builtin_bit_cast(h8, uint4{A0[0], A0[1], A0[0], A0[1]});
+            const h8 At1 = __builtin_bit_cast(h8, uint4{A1[0], A1[1], A1[0], A1[1]});
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
-            acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
+            for (int m = 0; m < MT; ++m) {
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At0, Bf[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At1, Bf[m], acc[m][2 * c + 1], 0, 0, 0);
+            }
         }
     };
 
@@ -679,8 +735,9 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             k_unit(t + 2 * step, S);
         }
 
-        // -- online softmax (base 2); rows past a pair's limit are -inf
+        // -- online softmax (base 2)
         float x[MT][4];
+        bool nonfin = false;
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -688,12 +745,20 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 const h2 mh = __builtin_bit_cast(h2, mw[m][i >> 1]);
                 const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
                 x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
+                nonfin |= !__builtin_isfinite(x[m][i]);
             }
-        if (t + kSub > r_all) {
+        // careful slice: rows past a pair's limit, masked rows or non-finite
+        // scores; unseen rows (past the limit, mask -inf) become -inf
+        const bool careful = t + kSub > r_all || __builtin_amdgcn_ballot_w64(nonfin) != 0;
+        if (careful) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[m][i] = t + 4 * lg + i < lim[m] ? x[m][i] : -INFINITY;
+                for (int i = 0; i < 4; ++i) {
+                    const h2 mh = __builtin_bit_cast(h2, mw[m][i >> 1]);
+                    const bool seen = t + 4 * lg + i < lim[m] && (float)mh[i & 1] != -INFINITY;
+                    x[m][i] = seen ? x[m][i] : -INFINITY;
+                }
         }
         bool grow = false;
         float mnew[MT];
@@ -713,16 +778,21 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 m_run[m] = mnew[m];
             }
         }
-        h2 P[MT][2];
+        float pw[MT][4];
+        h8 Bf[MT];  // F16/E5M2 V: weights as f16 high parts (products 0..3), low parts (4..7)
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const float mu = m_run[m] == -INFINITY ? 0.0f : m_run[m] + kPOff;
-            float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(x[m][i] - mu);
-            l_run[m] += (p[0] + p[1]) + (p[2] + p[3]);
-            P[m][0] = h2{(_Float16)p[0], (_Float16)p[1]};
-            P[m][1] = h2{(_Float16)p[2], (_Float16)p[3]};
+            for (int i = 0; i < 4; ++i) pw[m][i] = __builtin_amdgcn_exp2f(x[m][i] - mu);
+            l_run[m] += (pw[m][0] + pw[m][1]) + (pw[m][2] + pw[m][3]);
+            if constexpr (!QUANT) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    Bf[m][i] = (_Float16)pw[m][i];
+                    Bf[m][4 + i] = (_Float16)(pw[m][i] - (float)Bf[m][i]);
+                }
+            }
         }
         // -- V_j complete: later units K_j+1 + mask, V_j+1, K_j+2 + mask
         if (n2)
@@ -732,8 +802,45 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
+        // -- careful F16/E5M2 slice: a non-finite V element must not reach the
+        //    pairs that do not see its row through the shared V operand. Lane
+        //    (lr, lg) scans its sixteenth of rows 4lg..4lg+3; if any element is
+        //    Inf/NaN, the V operands are sanitised and each pair that sees a bad
+        //    row gets a NaN sum (its output becomes NaN, as ggml's would)
+        bool vsan = false;
+        if constexpr (!QUANT) {
+            if (careful) {
+                constexpr int ES = KT == XQ_TYPE_F16 ? 2 : 1;
+                constexpr int SPAN = ES * D / 16;  // bytes per lane per row (8..32)
+                const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
+                int rb = 0;
 #pragma unroll
-        for (int c = 0; c < NB; ++c) values(stage_tag, c, P);
+                for (int i = 0; i < 4; ++i) {
+                    const uint8_t* vr = Vs + (4 * lg + i) * REC + lr * SPAN;
+                    uint32_t bad = 0;
+#pragma unroll
+                    for (int k = 0; k < SPAN / 4; ++k) {
+                        const uint32_t w = lds_u32(vr + 4 * k);
+                        bad |= KT == XQ_TYPE_F16 ? f16x2_nonfinite(w) : e5m2x4_nonfinite(w);
+                    }
+                    rb |= bad ? 1 << i : 0;
+                }
+                rb |= dpp_i<0xB1>(rb);
+                rb |= dpp_i<0x4E>(rb);
+                rb |= dpp_i<0x141>(rb);
+                rb |= dpp_i<0x140>(rb);  // every lane of the row group: the flags of its four rows
+                vsan = __builtin_amdgcn_ballot_w64(rb != 0) != 0;
+                if (vsan) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (((rb >> i) & 1) && x[m][i] != -INFINITY) l_run[m] = NAN;
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, x, careful, Bf, vsan);
 
         // -- the V unit of slice j+2 into the stage this slice's V used
         if (n2) {
@@ -804,7 +911,21 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 float a1, inv, lse;
                 fa_finalize(Ls == 0.0f ? -INFINITY : Mn, Ls, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
                 float* od = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
-                *(f4*)(od + 4 * d4) = (o * a1) * inv;
+                f4 ov = (o * a1) * inv;
+                if (a.poison) {
+                    // the split reducer's rule with one split: a non-finite or
+                    // negative sum, factor, normaliser or output poisons the row.
+                    // A row's D/4 threads are one wave (D 256) or half of one (D 128).
+                    const bool bad = !__builtin_isfinite(Ls) || Ls < 0.0f || !__builtin_isfinite(inv) ||
+                                     (Ls != 0.0f && !__builtin_isfinite(lse)) || !__builtin_isfinite(ov[0]) ||
+                                     !__builtin_isfinite(ov[1]) || !__builtin_isfinite(ov[2]) || !__builtin_isfinite(ov[3]);
+                    const uint64_t rowmask = D == 256 ? ~0ull : (lane < 32 ? 0xffffffffull : 0xffffffff00000000ull);
+                    if (__builtin_amdgcn_ballot_w64(bad) & rowmask) {
+                        ov = f4{NAN, NAN, NAN, NAN};
+                        lse = NAN;
+                    }
+                }
+                *(f4*)(od + 4 * d4) = ov;
                 if (d4 == 0 && a.lse) a.lse[row] = lse;
             } else {
                 *(f4*)(a.part_o + (row * a.n_splits + split) * D + 4 * d4) = o;

@@ -60,6 +60,16 @@ constexpr int qimg_words(int qkm, int kt, int d) {
          : (d / 64) * 18 + 2 * (d / kQK);                        // lo/hi images + d_q + sum_q
 }
 
+// (query, head) pairs of a query tile: 32, except 16 at head dim 256 when the
+// GQA group fits in 16. Every tile of a head-dim-256 call then runs the same
+// 16-pair kernel variant (one wave count, one slice-to-wave assignment), so a
+// query's bits do not depend on how many queries share the call.
+constexpr int fa_max_pairs(int d, int g) { return d == 256 && g <= 16 ? 16 : 32; }
+// Queries per tile for a call with n_q queries and GQA group g.
+constexpr int fa_query_tile(int d, int g, int n_q) {
+    return g >= fa_max_pairs(d, g) ? 1 : (fa_max_pairs(d, g) / g < n_q ? fa_max_pairs(d, g) / g : n_q);
+}
+
 struct FaLaunch {
     const xq_tensor* q;
     const xq_tensor* k;

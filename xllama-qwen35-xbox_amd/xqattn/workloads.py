@@ -182,8 +182,9 @@ class FaConfig:
 
 FA_C1 = FaConfig("fa_decode_f16_h16kv8_d128_L4096", 1, 16, 8, 128, 4096, 1, F16)
 FA_C2 = FaConfig("fa_decode_q8_0_h24kv4_d256_L32768_b4", 1, 24, 4, 256, 32768, 4, Q8_0)
+# verify: mask padded to 16 rows (rows 8..15 all -inf, never read by the op)
 FA_C5 = FaConfig("fa_verify_q4_0_nq8_h32kv8_d128_L16392_b8", 8, 32, 8, 128, 16392, 8, Q4_0,
-                 causal_prefix=16384)
+                 causal_prefix=16384, n_q_pad=16)
 
 
 @dataclasses.dataclass(frozen=True)
