@@ -66,8 +66,6 @@ namespace xq {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef int i4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
@@ -135,20 +133,56 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
 
-// The signed bytes 0 and 1 of x as f32 (exact), two SDWA sign-extending
-// conversions (the compiler shifts before converting byte 1). The results feed
-// VALU instructions only, so no MFMA hazard hides in the asm.
-XQ_DEV void q8_pair_f32(uint32_t x, float& b0, float& b1) {
-    asm("v_cvt_f32_i32_sdwa %0, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f32_i32_sdwa %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
-        : "=&v"(b0), "=v"(b1)
-        : "v"(x));
+// V^T operands of one q8_0 block: the signed bytes 0 (tile 0) and 1 (tile 1)
+// of the rows' 16-bit words x0..x3 as f16 pairs (rows 0,1 and rows 2,3),
+// exact. Each pair is two SDWA conversions of sign-extended bytes, the second
+// writing the high half and keeping the low one. The trailing s_nop gives the
+// two wait states an MFMA reading a VGPR needs after a VALU wrote it (the
+// compiler's hazard tracking does not see into the asm).
+XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32_t (&A0)[2], uint32_t (&A1)[2]) {
+    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "s_nop 1"
+        : "=&v"(A0[0]), "=&v"(A0[1]), "=&v"(A1[0]), "=&v"(A1[1])
+        : "v"(x0), "v"(x1), "v"(x2), "v"(x3));
 }
 
-// bf16 bits of two f32 values whose low 16 bits are zero (exact), packed
-// (a in the low half).
-XQ_DEV uint32_t hi16_pair(float a, float b) {
-    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+// B operand of a quantized-V value product: the f32 weights w0..w3 (rows 0..3)
+// times the rows' f16 block scales, each formed in f32 by v_fma_mix and
+// rounded once to f16, packed as rows (0,1) and (2,3). The scale of row i is
+// the low (HI = false) or high half of d[i]. s_nop as in q8_vt_f16.
+template <bool HI>
+XQ_DEV void wd_f16(float w0, float w1, float w2, float w3, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                   uint32_t& b01, uint32_t& b23) {
+    if constexpr (HI)
+        asm("v_fma_mixlo_f16 %0, %2, %6, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %0, %3, %7, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %1, %4, %8, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %1, %5, %9, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "s_nop 1"
+            : "=&v"(b01), "=&v"(b23)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(d0), "v"(d1), "v"(d2), "v"(d3));
+    else
+        asm("v_fma_mixlo_f16 %0, %2, %6, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %0, %3, %7, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %1, %4, %8, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %1, %5, %9, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "s_nop 1"
+            : "=&v"(b01), "=&v"(b23)
+            : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(d0), "v"(d1), "v"(d2), "v"(d3));
+}
+
+// f16 exponent field of a block scale, 0 for Inf/NaN (those never size the
+// value scaling: a row that holds one and is seen makes its pairs NaN anyway).
+XQ_DEV int scale_exp(uint32_t h) {
+    const int e = (int)((h >> 10) & 31u);
+    return e == 31 ? 0 : e;
 }
 
 // Halves of w (a pair of f16) that are Inf or NaN (all-ones exponent) set to 0.
@@ -593,10 +627,10 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x W^T, the 32
     //      products of a lane group being its four rows' weight high parts, then
     //      their low parts (the V operand repeats the four rows)
-    //      pw: f32 weights (row 4lg + i, pair 16m + lr); xs: their scores (-inf
-    //      for rows the pair does not see); Bf: F16/E5M2 weight operands;
-    //      careful / vsan: the slice's careful mode and V sanitising
-    auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], const float (&xs)[MT][4], bool careful,
+    //      pw: f32 weights (row 4lg + i, pair 16m + lr; quantized V: times
+    //      2^S_p); seenm: careful slice's masks of the rows the pair sees;
+    //      Bf: F16/E5M2 weight operands; vsan: V sanitising
+    auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], bool careful, const uint32_t (&seenm)[MT][2],
                       const h8 (&Bf)[MT], bool vsan) {
         constexpr int ST = decltype(st_tag)::value;
         const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
@@ -614,49 +648,47 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 X[e] = lds_u16(vr + 32 * c + 2 * lr);
         }
         if constexpr (QUANT) {
-            // d_v of rows 4lg + i, block c, in f32 (exact)
-            float dv[4];
+            // B: w * 2^S * d_v rounded once to f16 (rows (0,1), (2,3)); the
+            // wave's power of two 2^S keeps every product in f16's normal range
+            uint32_t dvw[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t w = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
-                dv[i] = f16_bits_to_f32(((BB * c) & 2) ? w >> 16 : w & 0xffffu);
-            }
-            // B: w * d_v in f32, split into bf16 high (truncated, exact) and
-            // low (the exact remainder rounded to bf16) parts
-            bf8 Bq[MT];
+            for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
+            const bool dhi = ((BB * c) & 2) != 0;  // the scale sits in the high half of its dword
+            h4 Bv[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                float xv[4], lo[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    xv[i] = pw[m][i] * dv[i];
-                    if (careful) xv[i] = xs[m][i] == -INFINITY ? 0.0f : xv[i];  // unseen rows add nothing, whatever d_v is
-                    lo[i] = xv[i] - __uint_as_float(__float_as_uint(xv[i]) & 0xffff0000u);
+                uint32_t b01, b23;
+                if (dhi)
+                    wd_f16<true>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
+                else
+                    wd_f16<false>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
+                if (careful) {  // rows the pair does not see add 0, whatever their scale holds
+                    b01 &= seenm[m][0];
+                    b23 &= seenm[m][1];
                 }
-                const bf2 l01 = {(__bf16)lo[0], (__bf16)lo[1]}, l23 = {(__bf16)lo[2], (__bf16)lo[3]};
-                Bq[m] = __builtin_bit_cast(bf8, uint4{hi16_pair(xv[0], xv[1]), hi16_pair(xv[2], xv[3]),
-                                                      __builtin_bit_cast(uint32_t, l01),
-                                                      __builtin_bit_cast(uint32_t, l23)});
+                Bv[m] = __builtin_bit_cast(h4, uint2{b01, b23});
             }
-            // A: the integer values of tile t's dims in rows 4lg..4lg+3 as bf16 (exact)
-            float f0[4], f1[4];
+            // A: the integer values of tile t's dims in rows (0,1), (2,3) as f16 (exact)
+            uint32_t A0[2], A1[2];
+            if constexpr (KT == XQ_TYPE_Q8_0) {
+                q8_vt_f16(X[0], X[1], X[2], X[3], A0, A1);
+            } else {  // q4_0: low nibble (dim lr of the block), high nibble (dim 16 + lr), 1024 + n - 1032
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                if constexpr (KT == XQ_TYPE_Q8_0) {
-                    q8_pair_f32(X[e], f0[e], f1[e]);
-                } else {  // q4_0: low nibble (dim lr of the block), high nibble (dim 16 + lr)
-                    f0[e] = (float)((int)(X[e] & 15u) - 8);
-                    f1[e] = (float)((int)(X[e] >> 4) - 8);
+                for (int e = 0; e < 2; ++e) {
+                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+                    const uint32_t w = X[2 * e] | (X[2 * e + 1] << 16);
+                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
+                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
+                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
+                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
                 }
             }
-            const uint32_t a01 = hi16_pair(f0[0], f0[1]), a23 = hi16_pair(f0[2], f0[3]);
-            const uint32_t b01 = hi16_pair(f1[0], f1[1]), b23 = hi16_pair(f1[2], f1[3]);
-            const bf8 At0 = __builtin_bit_cast(bf8, uint4{a01, a23, a01, a23});
-            const bf8 At1 = __builtin_bit_cast(bf8, uint4{b01, b23, b01, b23});
+            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
+            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(At0, Bq[m], acc[m][2 * c], 0, 0, 0);
-                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(At1, Bq[m], acc[m][2 * c + 1], 0, 0, 0);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
             }
         } else {
             // A: f16 pairs of rows (0,1), (2,3) of tiles t = 0, 1 (exact)
@@ -695,6 +727,20 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // without a partner while the workgroup waits for them. Each wave posts its
     // progress and takes issue priority while it is behind its partner (ties go
     // to the younger wave).
+    // quantized V: pair p's accumulators hold sum w * 2^S_p * d_v * q, with
+    // S_p = 25 - the largest block-scale exponent field among the rows p has
+    // seen so far (so w * 2^S_p * |d_v| < 2^15). S_p depends on p's rows only,
+    // so a pair's bits do not depend on the pairs that share its tile; it only
+    // falls, and every fall rescales p's accumulator column by a power of two.
+    int e_max[MT], s_exp[MT];
+    float wscale[MT];
+    int e_min = -1;  // wave-uniform: the smallest e_max over the pairs (-1 while one has seen no row)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        e_max[m] = -1;
+        s_exp[m] = 0;
+        wscale[m] = 1.0f;
+    }
     int done = 0;
     if (lane == 0) sProg[wave] = 0;
     auto balance = [&]() {
@@ -735,18 +781,41 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             k_unit(t + 2 * step, S);
         }
 
+        // -- V_j complete: later units K_j+1 + mask, V_j+1, K_j+2 + mask
+        if (n2)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * NIS + 4 * MT) : "memory");
+        else if (n1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        // quantized V: lane l reads the block scales of row l/4 (largest exponent
+        // field er), used after the softmax
+        int er = 0;
+        if constexpr (QUANT) {
+            const uint8_t* vr = ring + S * 2 * SLICE + SLICE + (lane >> 2) * REC;
+            if constexpr (NB == 8) {
+                const int b0 = 2 * (lane & 3);
+                er = max(scale_exp(lds_u16(vr + BB * b0)), scale_exp(lds_u16(vr + BB * (b0 + 1))));
+            } else {
+                er = scale_exp(lds_u16(vr + BB * (lane & 3)));
+            }
+        }
         // -- online softmax (base 2)
         float x[MT][4];
         bool nonfin = false;
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int m = 0; m < MT; ++m) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const h2 mh = __builtin_bit_cast(h2, mw[m][i >> 1]);
                 const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
                 x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
-                nonfin |= !__builtin_isfinite(x[m][i]);
             }
+            // a sum of finite scores (|x| far below the f32 range) is finite
+            // exactly when every score is: one test for -inf, +inf and NaN
+            nonfin |= !__builtin_isfinite((x[m][0] + x[m][1]) + (x[m][2] + x[m][3]));
+        }
         // careful slice: rows past a pair's limit, masked rows or non-finite
         // scores; unseen rows (past the limit, mask -inf) become -inf
         const bool careful = t + kSub > r_all || __builtin_amdgcn_ballot_w64(nonfin) != 0;
@@ -794,14 +863,82 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 }
             }
         }
-        // -- V_j complete: later units K_j+1 + mask, V_j+1, K_j+2 + mask
-        if (n2)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * NIS + 4 * MT) : "memory");
-        else if (n1)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NIS + 2 * MT) : "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_wave_barrier();
+        // -- quantized V: each pair's largest block-scale exponent over the rows
+        //    of this slice it sees; lane l reads blocks of row l/4, a quad holds
+        //    its row's maximum, every lane gathers its lane group's four rows
+        uint32_t seenmask[MT][2];  // careful slice: f16-half masks of the rows the pair sees
+        if constexpr (QUANT) {
+            // fast test: no row's scale exceeds every pair's bound, so no pair's
+            // S moves (the exact per-pair update below runs only otherwise)
+            if (__builtin_amdgcn_ballot_w64(er > e_min)) {
+                er = max(er, dpp_i<0xB1>(er));
+                er = max(er, dpp_i<0x4E>(er));  // quad q holds row q's largest exponent
+                int ep[MT];
+                if (!careful) {
+                    // every pair sees every row: the slice's maximum, wave-wide
+                    int e = max(er, dpp_i<0x141>(er));
+                    e = max(e, dpp_i<0x140>(e));
+                    auto r = __builtin_amdgcn_permlane32_swap((uint32_t)e, (uint32_t)e, false, false);
+                    e = max((int)r[0], (int)r[1]);
+                    auto q = __builtin_amdgcn_permlane16_swap((uint32_t)e, (uint32_t)e, false, false);
+                    e = __builtin_amdgcn_readfirstlane(max((int)q[0], (int)q[1]));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) ep[m] = e;
+                } else {
+                    // the rows the pair sees: gather the lane group's four rows
+                    int erow[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) erow[i] = __shfl(er, (lane & ~15) + 4 * i);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        int e = -1;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) e = max(e, x[m][i] != -INFINITY ? erow[i] : -1);
+                        auto r = __builtin_amdgcn_permlane32_swap((uint32_t)e, (uint32_t)e, false, false);
+                        e = max((int)r[0], (int)r[1]);
+                        auto q = __builtin_amdgcn_permlane16_swap((uint32_t)e, (uint32_t)e, false, false);
+                        ep[m] = max((int)q[0], (int)q[1]);
+                    }
+                }
+                int emn = 1 << 30;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const bool grow = ep[m] > e_max[m];
+                    if (__builtin_amdgcn_ballot_w64(grow)) {
+                        const int s_new = grow ? 25 - max(ep[m], 1) : s_exp[m];
+                        const float f = __builtin_ldexpf(1.0f, s_new - s_exp[m]);  // exact power of two
+#pragma unroll
+                        for (int n = 0; n < 2 * NB; ++n) acc[m][n] *= f;
+                        s_exp[m] = s_new;
+                        wscale[m] = __builtin_ldexpf(1.0f, s_new);
+                        e_max[m] = grow ? ep[m] : e_max[m];
+                    }
+                    emn = min(emn, e_max[m]);
+                }
+                emn = min(emn, dpp_i<0xB1>(emn));
+                emn = min(emn, dpp_i<0x4E>(emn));
+                emn = min(emn, dpp_i<0x141>(emn));
+                emn = min(emn, dpp_i<0x140>(emn));
+                {
+                    auto r = __builtin_amdgcn_permlane32_swap((uint32_t)emn, (uint32_t)emn, false, false);
+                    emn = min((int)r[0], (int)r[1]);
+                    auto q = __builtin_amdgcn_permlane16_swap((uint32_t)emn, (uint32_t)emn, false, false);
+                    e_min = __builtin_amdgcn_readfirstlane(min((int)q[0], (int)q[1]));
+                }
+            }
+            if (careful) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    seenmask[m][0] = (x[m][0] != -INFINITY ? 0xffffu : 0u) | (x[m][1] != -INFINITY ? 0xffff0000u : 0u);
+                    seenmask[m][1] = (x[m][2] != -INFINITY ? 0xffffu : 0u) | (x[m][3] != -INFINITY ? 0xffff0000u : 0u);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pw[m][i] *= wscale[m];
+            }
+        }
         // -- careful F16/E5M2 slice: a non-finite V element must not reach the
         //    pairs that do not see its row through the shared V operand. Lane
         //    (lr, lg) scans its sixteenth of rows 4lg..4lg+3; if any element is
@@ -840,7 +977,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             }
         }
 #pragma unroll
-        for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, x, careful, Bf, vsan);
+        for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, careful, seenmask, Bf, vsan);
 
         // -- the V unit of slice j+2 into the stage this slice's V used
         if (n2) {
@@ -872,12 +1009,14 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             sL[wave][16 * m + lr] = lt;
         }
         float* mw = mb + (wave * 16 + lr) * MS;
+        const float unscale = __builtin_ldexpf(1.0f, -s_exp[m]);  // quantized V: undo 2^S_p (exact)
         // the lane's dims of block c as 16-byte writes (acc_dim's layout);
         // padding pairs are never read
         if (16 * m + lr < npa) {
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
-                const f4 x0 = acc[m][2 * c], x1 = acc[m][2 * c + 1];
+                const f4 x0 = QUANT ? acc[m][2 * c] * unscale : acc[m][2 * c];
+                const f4 x1 = QUANT ? acc[m][2 * c + 1] * unscale : acc[m][2 * c + 1];
                 if constexpr (KT == XQ_TYPE_Q4_0) {
                     *(f4*)(mw + acc_dim<KT>(c, 0, lg, 0)) = x0;
                     *(f4*)(mw + acc_dim<KT>(c, 1, lg, 0)) = x1;
