@@ -91,16 +91,28 @@ enum xq_fa_qk_policy {
 };
 
 /* KV split (split-K) policy. The partition never depends on the number of
- * queries, so a query's result does not depend on how many queries share the
- * call, and partial states are merged in ascending split order.
+ * queries, and a query tile's kernel variant (wave count, slice-to-wave
+ * assignment) depends on the head dim and GQA group only, so a query's result
+ * is bitwise independent of how many queries share the call
+ * (patches/0008-flash-attn-query-consistency.patch:40-56). Partial states
+ * are merged in ascending split order.
  *  XQ_FA_SPLIT_AUTO: MI355X policy, about 256 / (sequences x KV heads) splits
- *    (one workgroup per CU), rows a multiple of 16.
+ *    (one workgroup per CU), rows a multiple of 16. It depends on the number
+ *    of sequences and KV heads of the call: a sequence's bits can change with
+ *    the batch it is in.
+ *  The other modes depend on the KV length only (as the reference's do,
+ *  uwp/rkva/rkva-range-profile.h:99-107): under them a sequence's result is
+ *  also bitwise independent of the sequences batched with it.
  *  XQ_FA_SPLIT_REFERENCE: clamp(ceil(L/256), 1, 32) splits
  *    (uwp/rkva/rkva-range-profile.h:99-101).
  *  XQ_FA_SPLIT_BALANCED / FINE / COARSE: the reference's optimized modes
  *    1/2/3 (target rows, max splits) = (128,128) / (32,256) / (512,64)
  *    (uwp/rkva/rkva-range-profile.h:82-107).
- *  XQ_FA_SPLIT_NONE: one split (no reduce pass). */
+ *  XQ_FA_SPLIT_NONE: one split (no reduce pass).
+ *  XQ_FA_SPLIT_MQ_BALANCED / MQ_FINE: the reference's multi-query verify split
+ *    (q4_mq_split, uwp/rkva/rkva-range-profile.h:141-147): the balanced / fine
+ *    mode's rows rounded up to whole 64-row tiles, the count recomputed so no
+ *    split is empty (58128 rows: 114 x 512 / 228 x 256). */
 enum xq_fa_split_mode {
     XQ_FA_SPLIT_AUTO = 0,
     XQ_FA_SPLIT_REFERENCE = 1,
@@ -108,6 +120,8 @@ enum xq_fa_split_mode {
     XQ_FA_SPLIT_FINE = 3,
     XQ_FA_SPLIT_COARSE = 4,
     XQ_FA_SPLIT_NONE = 5,
+    XQ_FA_SPLIT_MQ_BALANCED = 6,
+    XQ_FA_SPLIT_MQ_FINE = 7,
 };
 
 /* Which pass-1 kernel computes the scores and the value product.

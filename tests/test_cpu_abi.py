@@ -54,10 +54,15 @@ def test_split_policy_reference_known_answers():
     assert sc(28672, xqattn.SPLIT_FINE) == 256
     assert sc(28672, xqattn.SPLIT_COARSE) == 56
     assert sc(1, xqattn.SPLIT_BALANCED) == 1
+    # the multi-query verify split (tests/rkva_range_profile_cpu.cpp:135-139)
+    assert sc(1, xqattn.SPLIT_MQ_BALANCED) == 1
+    assert (sc(58128, xqattn.SPLIT_MQ_BALANCED), xqattn.split_rows(58128, xqattn.SPLIT_MQ_BALANCED)) == (114, 512)
+    assert (sc(58128, xqattn.SPLIT_MQ_FINE), xqattn.split_rows(58128, xqattn.SPLIT_MQ_FINE)) == (228, 256)
 
 
 @pytest.mark.parametrize("mode", [xqattn.SPLIT_AUTO, xqattn.SPLIT_REFERENCE, xqattn.SPLIT_BALANCED,
-                                  xqattn.SPLIT_FINE, xqattn.SPLIT_COARSE, xqattn.SPLIT_NONE])
+                                  xqattn.SPLIT_FINE, xqattn.SPLIT_COARSE, xqattn.SPLIT_NONE,
+                                  xqattn.SPLIT_MQ_BALANCED, xqattn.SPLIT_MQ_FINE])
 def test_split_policy_covers_every_row(mode):
     for L in [1, 7, 16, 31, 32, 33, 128, 129, 255, 256, 257, 512, 1000, 4096, 4133, 16392, 28672, 32768, 131072]:
         k = xqattn.split_count(L, mode)
@@ -70,6 +75,11 @@ def test_split_policy_covers_every_row(mode):
             assert rows * (k - 1) < L  # the reference's own assertion for these lengths
         if mode == xqattn.SPLIT_NONE:
             assert k == 1
+        if mode in (xqattn.SPLIT_MQ_BALANCED, xqattn.SPLIT_MQ_FINE):
+            # whole 64-row tiles, no empty split, never more splits than the mode's
+            assert rows % 64 == 0 and rows * (k - 1) < L
+            base = xqattn.SPLIT_BALANCED if mode == xqattn.SPLIT_MQ_BALANCED else xqattn.SPLIT_FINE
+            assert k <= xqattn.split_count(L, base)
 
 
 def test_split_policy_matches_reference_header():
@@ -84,6 +94,11 @@ def test_split_policy_matches_reference_header():
             assert xqattn.split_count(L, m) == k, (L, m)
             if L:
                 assert xqattn.split_rows(L, m) == ref.xr_split_rows(L, k), (L, m)
+        kk, rr = ctypes.c_uint32(), ctypes.c_uint32()
+        for m, rm in {xqattn.SPLIT_MQ_BALANCED: 1, xqattn.SPLIT_MQ_FINE: 2}.items():
+            ref.xr_q4_mq_split(L, rm, ctypes.byref(kk), ctypes.byref(rr))
+            if L:
+                assert (xqattn.split_count(L, m), xqattn.split_rows(L, m)) == (kk.value, rr.value), (L, m)
 
 
 def _desc(typ, ne, nb=None, esize=None):

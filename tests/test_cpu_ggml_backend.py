@@ -113,3 +113,44 @@ int main(void) {
             xqattn.XqGgmlNode.src.offset, ctypes.sizeof(xqattn.XqGgmlNode),
             ctypes.sizeof(xqattn.XqGgmlBackendParams), ctypes.sizeof(xqattn.XqFaParams)]
     assert got == want
+
+
+def test_gdn_contract_flips_of_the_reference_test():
+    """The reference's own flip sequence on one T = 3, slots = 5 node
+    (tests/test_ggml_d3d12.cpp:238-271), each flip undone before the next:
+    rows-indexed src[6], raw gates, 18 slots, the KDA vector gate
+    g->ne[0] = 128, F16 q, a q row stride that is not float-aligned, and a
+    sequence count that differs between operands; the restored node is
+    supported again. Each flip is checked through the ggml face and, where it is
+    an operand flip, through the direct predicate."""
+    T, slots = 3, 5
+    q, k, v, g, beta, s, dst = _gdn_descs(T=T, B=1, slots=slots)
+    assert (dst.ne[0], dst.ne[1]) == (4096, T + slots * 128)
+
+    def node(**kw):
+        return xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, kw.get("slots", slots),
+                                               raw_gates=kw.get("raw", 0))
+
+    def direct(sl=slots, raw=0):
+        return bool(xqattn.load().xq_supports_gated_delta_net(
+            *(ctypes.byref(x) for x in (q, k, v, g, beta, s, dst)), sl, raw))
+
+    assert xqattn.ggml_supports_op(node()) and direct()
+    n = node()
+    n.srcs += [q]  # src[6]: rows-indexed mode
+    assert not xqattn.ggml_supports_op(n)
+    assert not xqattn.ggml_supports_op(node(raw=1)) and not direct(raw=1)
+    assert not direct(sl=18)
+    g.ne[0] = 128  # KDA vector gate
+    assert not xqattn.ggml_supports_op(node()) and not direct()
+    g.ne[0] = 1
+    q.type = wl.F16
+    assert not xqattn.ggml_supports_op(node()) and not direct()
+    q.type = wl.F32
+    q.nb[1] += 1  # cannot be expressed in float indices
+    assert not xqattn.ggml_supports_op(node()) and not direct()
+    q.nb[1] -= 1
+    v.ne[3] = 2
+    assert not xqattn.ggml_supports_op(node()) and not direct()
+    v.ne[3] = 1
+    assert xqattn.ggml_supports_op(node()) and direct()

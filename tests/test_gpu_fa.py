@@ -48,7 +48,8 @@ def test_fa_config_parity(torch_gpu, cfg, engine):
 
 @pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
 @pytest.mark.parametrize("split_mode", [xqattn.SPLIT_REFERENCE, xqattn.SPLIT_FINE, xqattn.SPLIT_NONE,
-                                        xqattn.SPLIT_BALANCED, xqattn.SPLIT_COARSE])
+                                        xqattn.SPLIT_BALANCED, xqattn.SPLIT_COARSE, xqattn.SPLIT_MQ_BALANCED,
+                                        xqattn.SPLIT_MQ_FINE])
 def test_fa_split_modes(torch_gpu, split_mode, engine):
     cfg = wl.FaConfig("q8_split", 1, 24, 4, 256, 5000, 2, wl.Q8_0)
     case_note(f"split mode {split_mode} engine {engine}")

@@ -113,6 +113,16 @@ void split_policy(int64_t L, int mode, int64_t n_seq_heads, int32_t* n_splits, i
     case XQ_FA_SPLIT_BALANCED: k = opt_split_k(L, 1); r = cdiv(L, k); break;
     case XQ_FA_SPLIT_FINE: k = opt_split_k(L, 2); r = cdiv(L, k); break;
     case XQ_FA_SPLIT_COARSE: k = opt_split_k(L, 3); r = cdiv(L, k); break;
+    // the reference's multi-query verify split (uwp/rkva/rkva-range-profile.h:
+    // 141-147): the mode's rows rounded up to whole 64-row tiles, then the
+    // split count recomputed so no split is empty
+    case XQ_FA_SPLIT_MQ_BALANCED:
+    case XQ_FA_SPLIT_MQ_FINE: {
+        const int64_t k0 = opt_split_k(L, mode == XQ_FA_SPLIT_MQ_BALANCED ? 1 : 2);
+        r = cdiv(cdiv(L, k0), 64) * 64;
+        k = cdiv(L, r);
+        break;
+    }
     case XQ_FA_SPLIT_NONE:
     default: r = L; k = 1; break;
     }
@@ -141,7 +151,7 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
         return fail(XQ_ERR_UNSUPPORTED, "k/v type %d/%d not supported (F16, Q8_0, Q4_0, E5M2; same type)", k->type, v->type);
     if (p->qk_policy != XQ_FA_QK_CONSISTENT && p->qk_policy != XQ_FA_QK_NATIVE)
         return fail(XQ_ERR_BAD_ARG, "bad qk_policy %d", p->qk_policy);
-    if (p->split_mode < XQ_FA_SPLIT_AUTO || p->split_mode > XQ_FA_SPLIT_NONE)
+    if (p->split_mode < XQ_FA_SPLIT_AUTO || p->split_mode > XQ_FA_SPLIT_MQ_FINE)
         return fail(XQ_ERR_BAD_ARG, "bad split_mode %d", p->split_mode);
     if (p->engine < XQ_FA_ENGINE_AUTO || p->engine > XQ_FA_ENGINE_VALU)
         return fail(XQ_ERR_BAD_ARG, "bad engine %d", p->engine);

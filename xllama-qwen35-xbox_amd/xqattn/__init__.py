@@ -31,6 +31,7 @@ STATUS = {0: "OK", 1: "UNSUPPORTED", 2: "BAD_SHAPE", 3: "BAD_ARG", 4: "WORKSPACE
 
 QK_CONSISTENT, QK_NATIVE = 0, 1
 SPLIT_AUTO, SPLIT_REFERENCE, SPLIT_BALANCED, SPLIT_FINE, SPLIT_COARSE, SPLIT_NONE = range(6)
+SPLIT_MQ_BALANCED, SPLIT_MQ_FINE = 6, 7
 GDN_AUTO, GDN_STEP, GDN_CHUNKED = 0, 1, 2
 ENGINE_AUTO, ENGINE_MFMA, ENGINE_VALU = 0, 1, 2
 
