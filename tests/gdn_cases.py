@@ -61,11 +61,15 @@ def _selftest_inputs(T, B, seed=1701):
     return q, k, v, g, beta, st
 
 
-def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False) -> GdnCase:
+def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False, v_scale=1.0) -> GdnCase:
+    """v_scale multiplies v and the initial state (the recurrence is linear in them)."""
     if dist == "selftest":
         q, k, v, g, beta, st = _selftest_inputs(T, B)
     else:
         q, k, v, g, beta, st = wl.gdn_inputs(wl.GdnConfig("case", T, B, slots, bf16), seed=seed)
+    if v_scale != 1.0:
+        v = (v * np.float32(v_scale)).astype(np.float32)
+        st = (st * np.float32(v_scale)).astype(np.float32)
     typ = wl.BF16 if bf16 else wl.F32
     if bf16:
         q, k, v = (oracle.f32_to_bf16(a) for a in (q, k, v))

@@ -107,3 +107,21 @@ def test_gdn_chunked_strong_decay(torch_gpu):
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     _check(case, got, case.oracle_f64(), "chunked strong decay")
 
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("v_scale", [1e-6, 1e-3, 1e3, 1e6])
+def test_gdn_chunked_magnitude_sweep(torch_gpu, v_scale, bf16):
+    """v and the initial state scaled by 1e-6 .. 1e6 (q, k L2-normalised, as the
+    model gives them): the per-column-block power of two keeps the f16 operands
+    in range, so the reference selftest's bar max|gpu - want| / max|want| <= 1e-4
+    holds against the float64 recurrence at every scale."""
+    case_note(f"gdn chunked magnitude v_scale={v_scale} bf16={bf16}")
+    case = make_gdn_case(200, 1, B=1, dist="north_star", bf16=bf16, seed=41, v_scale=v_scale)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    want = case.oracle_f64()
+    v = _valid_rows(case)
+    assert np.all(np.isfinite(got[:, :v]))
+    rel = np.abs(got[:, :v] - want[:, :v]).max() / np.abs(want[:, :v]).max()
+    print(f"v_scale={v_scale} bf16={bf16}: rel {rel:.2e}")
+    assert rel <= 1e-4, rel

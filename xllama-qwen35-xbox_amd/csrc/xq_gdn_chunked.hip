@@ -19,11 +19,13 @@
 //   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
 //                   parallel: K K^T on f16 MFMA (f32 accumulation) and the unit
 //                   lower-triangular solve for T in f32; stores T as f16 hi + lo
-//                   planes, the decay vectors and the cumulative log-decays G
-//                   (17 KB per chunk) in the workspace. f32 k rows enter as f16
-//                   hi + lo (the products take hi*hi + hi*lo + lo*hi); bf16
-//                   rows are f16 values already (their 8 significant bits fit,
-//                   down to 2^-24).
+//                   planes, the decay vectors, the cumulative log-decays G and
+//                   the chunk's largest |v| per 16-column block (17 KB per
+//                   chunk) in the workspace. f32 k rows enter as f16 hi + lo
+//                   (the products take hi*hi + hi*lo + lo*hi); bf16 rows enter
+//                   as f16 (their 8 significant bits fit; a bf16 value below
+//                   2^-14 keeps an absolute precision of 2^-25 there, not its
+//                   relative one).
 //   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
 //                   the chunks in order with its 128 x 16 state block in
 //                   registers (f32). Every MFMA operand that does not depend on
@@ -41,6 +43,16 @@
 //                   f32-recurrence tolerances.
 // The 8 column blocks of a head run on one XCD (consecutive logical workgroups)
 // so the chunk rows and T, P they share are read from HBM once.
+//
+// Range. The recurrence is linear in (V, S): the scan runs on V and S times a
+// power of two 2^a per (sequence, v-head, column block), chosen from the largest
+// |v| of the column block over the prefill and the largest |S| entering it so
+// that they lie in [1, 2), and divides Y and the final state by 2^a (exact). V
+// and the state may so have any f32 magnitude: f16's range holds a state that
+// grows 2^15-fold beyond them. q and k rows enter as f16 (or hi + lo): they
+// must lie in the L2-normalised range the model gives them (|element| below
+// 65504; beyond it the f16 operands are Inf and the outputs Inf/NaN), and each
+// element keeps an absolute precision of about 2^-25.
 #include <type_traits>
 
 #include "xq_kernels.h"
@@ -58,8 +70,9 @@ constexpr int kColBlocks = 128 / kCols;
 // Workspace record of one (sequence, v-head, chunk), byte offsets.
 constexpr int kRecTHi = 0;                       // f16 [64][64]
 constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
-constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, G[64] at 192
+constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, max|v|[8] at 136, G[64] at 192
 constexpr int kRecG = 192;                      // G offset in floats within the decays
+constexpr int kRecVmax = 136;                   // largest |v| of the chunk per 16-column block (floats)
 constexpr int kRecBytes = kRecDec + 1024;
 
 struct GdnChunkArgs {
@@ -140,6 +153,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][FP]
     __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // K K^T, then L
     __shared__ float sG[64], sBeta[64], sEG[64];
+    __shared__ uint32_t sVmax[kColBlocks];  // bits of the largest |v| per column block
     // f32 rows: the f16 remainders of K
     constexpr int NKL = BF16 ? 8 : 64 * KP;
     __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
@@ -172,6 +186,23 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             *(h8*)(sK + t * KP + i0) = hk;
             if constexpr (!BF16) *(h8*)(sKl + t * KP + i0) = lo_h8(xk, hk);
         }
+        // largest |v| of the token's 32 columns 32qt.. (two column blocks); a
+        // NaN compares as the largest bits, so it reaches the scan's choice
+        if (tid < kColBlocks) sVmax[tid] = 0;
+        uint32_t vm[2] = {0, 0};
+        if (ok) {
+            const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tg * a.v_nb2 + (int64_t)h * a.v_nb1;
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                float xv[8];
+                load8<BF16, false>(vr, 32 * qt + 8 * gi, xv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vm[gi >> 1] = max(vm[gi >> 1], __float_as_uint(xv[e]) & 0x7fffffffu);
+            }
+        }
+        __syncthreads();  // sVmax cleared
+        atomicMax(&sVmax[2 * qt], vm[0]);
+        atomicMax(&sVmax[2 * qt + 1], vm[1]);
         if (tid < 64) {
             const int tt = t0 + tid;
             const bool ok2 = tt < a.T;
@@ -283,6 +314,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         dec[64 + tid] = __expf(GC - G);
         dec[kRecG + tid] = G;
         if (tid == 0) dec[128] = __expf(GC);
+        if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[tid]);
     }
 }
 
@@ -461,6 +493,42 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     }
     float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
 
+    // ---- 2^a: the largest |S| entering the block and |v| of its columns over
+    //      the prefill (the chunks' maxima from the prep) brought into [1, 2)
+    __shared__ uint32_t sAm[4];
+    {
+        uint32_t am = 0;
+#pragma unroll
+        for (int a2 = 0; a2 < 2; ++a2)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) am = max(am, __float_as_uint(S[a2][r]) & 0x7fffffffu);
+        for (int n = lane; n < a.n_chunks; n += 64) {
+            const float* dec = (const float*)(a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes + kRecDec);
+            am = max(am, __float_as_uint(dec[kRecVmax + cb]) & 0x7fffffffu);
+        }
+        am = max(am, (uint32_t)dpp_i<0xB1>((int)am));
+        am = max(am, (uint32_t)dpp_i<0x4E>((int)am));
+        am = max(am, (uint32_t)dpp_i<0x141>((int)am));
+        am = max(am, (uint32_t)dpp_i<0x140>((int)am));
+        am = max(am, (uint32_t)__shfl_xor((int)am, 16));
+        am = max(am, (uint32_t)__shfl_xor((int)am, 32));
+        if (lane == 0) sAm[wave] = am;
+    }
+    __syncthreads();
+    int pa = 0;  // the power a
+    {
+        const float m = __uint_as_float(max(max(sAm[0], sAm[1]), max(sAm[2], sAm[3])));
+        if (m > 0.0f && __builtin_isfinite(m)) {
+            int ex;
+            (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
+            pa = min(max(1 - ex, -100), 100);
+        }
+    }
+    const float vscale = __builtin_ldexpf(1.0f, pa), unscale = __builtin_ldexpf(1.0f, -pa);
+    const float yscale = a.scale * unscale;
+#pragma unroll
+    for (int a2 = 0; a2 < 2; ++a2) S[a2] *= vscale;
+
     ScanOps<BF16, VEC> ops[2];
     scan_load_all<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
     // One chunk: C holds its operands (loaded a chunk ahead), the next chunk's
@@ -522,7 +590,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         const float egr[4] = {C.eg.x, C.eg.y, C.eg.z, C.eg.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float vv = (C.vok >> r) & 1 ? (BF16 ? bf16_bits_to_f32(C.vw[r]) : __uint_as_float(C.vw[r])) : 0.0f;
+            const float vv =
+                (C.vok >> r) & 1 ? (BF16 ? bf16_bits_to_f32(C.vw[r]) : __uint_as_float(C.vw[r])) * vscale : 0.0f;
             const float x = vv - egr[r] * (ksh[r] + ksl[r]);
             QS[r] = egr[r] * (qsh[r] + qsl[r]);
             xh[r] = f16_hi(x), xl[r] = f16_lo(x);
@@ -605,7 +674,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = nn * kChunk + 16 * wave + 4 * lg + r;
-            if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * a.scale;
+            if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * yscale;
         }
 
         // ---- S = e^{G_C} S + K^T (e^{G_C - G} U) for this wave's key-dim tiles
@@ -641,7 +710,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     for (int a2 = 0; a2 < 2; ++a2) {
         const int it = 2 * wave + a2;
         *(float4*)(so + (int64_t)(kCols * cb + lr) * 128 + 16 * it + 4 * lg) =
-            make_float4(S[a2][0], S[a2][1], S[a2][2], S[a2][3]);
+            make_float4(S[a2][0] * unscale, S[a2][1] * unscale, S[a2][2] * unscale, S[a2][3] * unscale);
     }
 }
 
