@@ -177,6 +177,20 @@ xq_status xq_flash_attn_ext(const xq_tensor* q, const xq_tensor* k, const xq_ten
                             float* lse, const xq_fa_params* params, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* xq_flash_attn_ext without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. It
+ * allocates nothing: its workspace is a 32 MiB array in the library's device
+ * image, one per GPU, whose address is looked up on the first call on a device
+ * (the current device must be the stream's). Calls whose workspace
+ * (xq_flash_attn_ext_workspace) exceeds 32 MiB return XQ_ERR_WORKSPACE before
+ * any launch. Every call on a GPU shares that GPU's array (nothing in it needs
+ * to start zeroed): calls that overlap on one GPU race and must be ordered by
+ * the caller. Results equal xq_flash_attn_ext's bit for bit. */
+xq_status xq_flash_attn_ext_noalloc(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
+                                    const xq_tensor* mask, const xq_tensor* sinks, xq_tensor* dst,
+                                    float* lse, const xq_fa_params* params, void* stream);
+
 /* Range attention (the remote-KV-attention engine's attend_range,
  * uwp/rkva/remote-attn-engine.h:152-154 and op RKVA_RANGE_ATTN,
  * uwp/rkva/remote-attn-protocol.h:228-237). KV rows are compact: row r holds

@@ -6,9 +6,18 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "xq_kernels.h"
+
+// ------------------------------------------------------------ no-alloc scratch
+// The workspace of xq_flash_attn_ext_noalloc: one array per GPU, part of the
+// library's device image (each GPU the library runs on holds it until the
+// process ends). Host code reaches it only through the per-device address
+// hipGetSymbolAddress returns (the array's name is not a device address).
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
@@ -310,6 +319,45 @@ xq_status xq_flash_attn_ext(const xq_tensor* q, const xq_tensor* k, const xq_ten
     const hipError_t e = xq::fa_launch(L, (hipStream_t)stream);
     if (e != hipSuccess) return fail(XQ_ERR_HIP, "flash_attn_ext launch: %s", hipGetErrorString(e));
     return ok();
+}
+
+// The scratch array's address on the current device, looked up once per device
+// (with that device current) and kept.
+static hipError_t scratch_address(void** out) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
+xq_status xq_flash_attn_ext_noalloc(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
+                                    const xq_tensor* mask, const xq_tensor* sinks, xq_tensor* dst,
+                                    float* lse, const xq_fa_params* params, void* stream) {
+    FaPlan P;
+    const xq_status st = fa_check(q, k, v, mask, sinks, dst, params, &P);
+    if (st != XQ_OK) return st;
+    if (P.ws > kScratchBytes)
+        return fail(XQ_ERR_WORKSPACE,
+                    "call needs %zu bytes of workspace; the no-alloc entry's scratch holds %zu bytes per GPU "
+                    "(use xq_flash_attn_ext with a caller workspace)",
+                    P.ws, kScratchBytes);
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) return fail(XQ_ERR_HIP, "scratch address: %s", hipGetErrorString(e));
+    xq::NoAllocScope no_events;
+    return xq_flash_attn_ext(q, k, v, mask, sinks, dst, lse, params, ws, kScratchBytes, stream);
 }
 
 // ------------------------------------------------------------ range attention

@@ -23,6 +23,13 @@ xq_status set_error(xq_status st, const char* msg);
 bool prof_events(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop);
 void prof_commit(const char* name, hipEvent_t start, hipEvent_t stop);
 
+// While one is alive on a thread, launches on that thread record no timing
+// events (the no-allocation entry point creates no HIP objects).
+struct NoAllocScope {
+    NoAllocScope();
+    ~NoAllocScope();
+};
+
 template <typename F, typename... Args>
 inline void launch(const char* name, F kernel, dim3 grid, dim3 block, hipStream_t stream, Args... args) {
     hipEvent_t start, stop;

@@ -24,10 +24,14 @@ std::atomic<int> g_on{0};
 std::mutex g_mu;
 std::vector<Pending> g_pending;
 std::map<std::string, Total> g_totals;
+thread_local int g_no_alloc = 0;
 }  // namespace
 
+NoAllocScope::NoAllocScope() { ++g_no_alloc; }
+NoAllocScope::~NoAllocScope() { --g_no_alloc; }
+
 bool prof_events(hipStream_t stream, hipEvent_t* start, hipEvent_t* stop) {
-    if (!g_on.load(std::memory_order_relaxed)) return false;
+    if (!g_on.load(std::memory_order_relaxed) || g_no_alloc) return false;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
     if (hipEventCreate(start) != hipSuccess) return false;

@@ -37,6 +37,7 @@ ENGINE_AUTO, ENGINE_MFMA, ENGINE_VALU = 0, 1, 2
 
 EXPORTS = (
     "xq_supports_flash_attn_ext", "xq_flash_attn_ext_workspace", "xq_flash_attn_ext",
+    "xq_flash_attn_ext_noalloc",
     "xq_fa_range_workspace", "xq_fa_range", "xq_fa_lse_merge", "xq_fa_split_count", "xq_fa_split_rows",
     "xq_supports_gated_delta_net", "xq_gated_delta_net_workspace", "xq_gated_delta_net",
     "xq_kv_store", "xq_kv_record_bytes", "xq_last_error", "xq_abi_version",
@@ -118,6 +119,7 @@ def load() -> ctypes.CDLL:
         "xq_supports_flash_attn_ext": (ctypes.c_int, [T, T, T, T, T, T, FP]),
         "xq_flash_attn_ext_workspace": (i32, [T, T, T, T, T, T, FP, ctypes.POINTER(sz)]),
         "xq_flash_attn_ext": (i32, [T, T, T, T, T, T, P, FP, P, sz, P]),
+        "xq_flash_attn_ext_noalloc": (i32, [T, T, T, T, T, T, P, FP, P]),
         "xq_fa_range_workspace": (i32, [i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(sz)]),
         "xq_fa_range": (i32, [P, P, i32, i32, P, P, i32, i32, i32, i32, i32, f32, i32, P, P, P, sz, P]),
         "xq_fa_lse_merge": (i32, [P, P, i32, i64, i32, P, P, P]),
@@ -261,6 +263,16 @@ def flash_attn_ext(q: DevTensor, k: DevTensor, v: DevTensor, mask, sinks, dst: D
                                     ctypes.byref(params), ctypes.c_void_p(wp), wn, _stream(stream)),
            "flash_attn_ext")
     return ws
+
+
+def flash_attn_ext_noalloc(q: DevTensor, k: DevTensor, v: DevTensor, mask, sinks, dst: DevTensor,
+                           params: XqFaParams, lse=None, stream=None):
+    """GGML_OP_FLASH_ATTN_EXT with the library's per-GPU scratch as workspace
+    (no allocation on any path)."""
+    ds = _keep(q, k, v, mask, sinks, dst)
+    refs = [ctypes.byref(x) if x is not None else None for x in ds]
+    _check(load().xq_flash_attn_ext_noalloc(*refs, ctypes.c_void_p(lse.data_ptr()) if lse is not None else None,
+                                            ctypes.byref(params), _stream(stream)), "flash_attn_ext_noalloc")
 
 
 def fa_range(q, positions, n_head, k, v, n_head_kv, head_dim, kv_type, origin, active, kq_scale,
