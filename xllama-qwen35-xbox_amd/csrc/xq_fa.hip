@@ -29,6 +29,8 @@
 // call (the purpose of patches/0006-…:7-11 and patches/0008-…:40-56). The
 // kernels are compiled with -ffp-contract=off and write every fused
 // multiply-add explicitly.
+#include <type_traits>
+
 #include "xq_fa_common.h"
 
 namespace xq {
@@ -541,83 +543,105 @@ __global__ __launch_bounds__(kThreads) void fa_pass1(FaArgs a, const uint32_t* _
     }
 }
 
-// One workgroup of D threads per (sequence, query, head) row; thread d owns
-// output dim d and sums the splits in ascending order. The split states are
-// loaded in parallel; the partial numerators are fetched CH splits at a time
-// so the loads are in flight together while the sum keeps its order. CH is 16
-// for up to 16 splits and 32 above, so the automatic policy's counts (up to 32)
-// take one memory round trip (32 splits of 4096 f16 rows: 7.2-7.7 -> 6.0-6.6 us
-// per reduce launch), while 16 splits run 0.45 us slower with the wider batch.
+// One wave per (sequence, query, head) row; lane owns dims VPL*lane ..
+// VPL*lane + VPL - 1 and walks the splits in ascending order with the same
+// (wave-uniform) split states and weights as every other lane, so the row
+// needs no barrier and no LDS. The states and the numerators of the first CH
+// splits are loaded together: one memory round trip for up to CH splits (the
+// automatic policy's counts), CH at a time beyond.
 template <int D, int CH>
-__global__ __launch_bounds__(D) void fa_reduce(FaArgs a) {
-    __shared__ float sm[kMaxSplits], sl[kMaxSplits], sw[kMaxSplits];
-    __shared__ float sMax[D / 64];
+__global__ __launch_bounds__(64) void fa_reduce(FaArgs a) {
+    constexpr int VPL = D / 64;
+    using V = typename std::conditional<VPL == 4, float4, float2>::type;
     const int64_t row = blockIdx.x;
     const int S = a.n_splits;
-    const int d = threadIdx.x;
+    const int lane = threadIdx.x;
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
     const int b = (int)(row / rows_per_seq);
     const int h = (int)(row % a.H);
-    // the numerators of the first CH splits are loaded together with the split
-    // states: one memory round trip for S <= CH
-    const float* po = a.part_o + row * S * D + d;
-    float v0[CH];
+    const float2* ml = a.part_ml + row * S;
+    const float* po = a.part_o + row * S * D + VPL * lane;
+    auto ldv = [&](int s) { return *(const V*)(po + (int64_t)s * D); };
+    float2 st[CH];
+    V v0[CH];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) v0[i] = i < S ? po[(int64_t)i * D] : 0.0f;
-    float mloc = -3.402823466e38f;
-    int bad = 0;
-    for (int s = d; s < S; s += D) {
-        const float2 ml = a.part_ml[row * S + s];
-        sm[s] = ml.x;
-        sl[s] = ml.y;
-        if (ml.y != 0.0f) {
-            if (!isfinite(ml.y) || ml.y < 0.0f || !isfinite(ml.x))
-                bad = 1;
-            else
-                mloc = fmaxf(mloc, ml.x);
-        }
+    for (int i = 0; i < CH; ++i) {
+        st[i] = i < S ? ml[i] : make_float2(0.0f, 0.0f);
+        v0[i] = i < S ? ldv(i) : V{};
     }
-    mloc = wave_max(mloc);
-    if (lane_id() == 0) sMax[d / 64] = mloc;
-    bad = __syncthreads_or(bad);
-    float M = sMax[0];
+    // participating splits (den != 0): the maximum; a non-finite or negative
+    // den or a non-finite maximum is bad (shaders/rkva/rkva_range_reduce_opt.hlsl:39-56)
+    float M = -3.402823466e38f;
+    bool bad = false;
+    auto visit = [&](float2 x) {
+        if (x.y != 0.0f) {
+            if (!__builtin_isfinite(x.y) || x.y < 0.0f || !__builtin_isfinite(x.x))
+                bad = true;
+            else
+                M = fmaxf(M, x.x);
+        }
+    };
 #pragma unroll
-    for (int w = 1; w < D / 64; ++w) M = fmaxf(M, sMax[w]);
-    for (int s = d; s < S; s += D) sw[s] = sl[s] != 0.0f ? expf(sm[s] - M) : 0.0f;
-    __syncthreads();
-    // every thread forms L (ascending split order) and the output factors itself
+    for (int i = 0; i < CH; ++i) visit(st[i]);
+    for (int s = CH; s < S; ++s) visit(ml[s]);
+    float w0[CH];
     float L = 0.0f;
-    for (int s = 0; s < S; ++s)
-        if (sl[s] != 0.0f) L = fmaf(sl[s], sw[s], L);
-    int badl = bad || !isfinite(L);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        w0[i] = st[i].y != 0.0f ? expf(st[i].x - M) : 0.0f;
+        if (st[i].y != 0.0f) L = fmaf(st[i].y, w0[i], L);
+    }
+    for (int s = CH; s < S; ++s) {
+        const float2 x = ml[s];
+        if (x.y != 0.0f) L = fmaf(x.y, expf(x.x - M), L);
+    }
     float a1, inv, lse;
     fa_finalize(L == 0.0f ? -INFINITY : M, L, a.sinks != nullptr, a.sinks ? a.sinks[h] : 0.0f, a1, inv, lse);
-    if (!isfinite(inv) || (L != 0.0f && !isfinite(lse))) badl = 1;
-    badl = badl && a.poison;
-    float acc = 0.0f;
+    bad = bad || !__builtin_isfinite(L) || !__builtin_isfinite(inv) || (L != 0.0f && !__builtin_isfinite(lse));
+    float acc[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) acc[j] = 0.0f;
+    auto add = [&](const V& v, float w) {
+        const float* e = (const float*)&v;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) acc[j] = fmaf(e[j], w, acc[j]);
+    };
 #pragma unroll
     for (int i = 0; i < CH; ++i)
-        if (i < S && sl[i] != 0.0f) acc = fmaf(v0[i], sw[i], acc);
+        if (st[i].y != 0.0f) add(v0[i], w0[i]);
     for (int s0 = CH; s0 < S; s0 += CH) {
-        float v[CH];
+        V v[CH];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) v[i] = (s0 + i < S) ? po[(int64_t)(s0 + i) * D] : 0.0f;
+        for (int i = 0; i < CH; ++i) v[i] = s0 + i < S ? ldv(s0 + i) : V{};
 #pragma unroll
-        for (int i = 0; i < CH; ++i)
-            if (s0 + i < S && sl[s0 + i] != 0.0f) acc = fmaf(v[i], sw[s0 + i], acc);
-    }
-    float out = (acc * a1) * inv;
-    if (a.poison) {
-        // any non-finite participating state or numerator poisons the whole row
-        if (__syncthreads_or(badl || !isfinite(out))) {
-            out = NAN;
-            lse = NAN;
+        for (int i = 0; i < CH; ++i) {
+            if (s0 + i >= S) break;
+            const float2 x = ml[s0 + i];
+            if (x.y != 0.0f) add(v[i], expf(x.x - M));
         }
     }
-    if (d == 0 && a.lse) a.lse[row] = lse;
+    float out[VPL];
+    bool nonfin = false;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        out[j] = (acc[j] * a1) * inv;
+        nonfin |= !__builtin_isfinite(out[j]);
+    }
+    // range calls: any non-finite participating state, numerator or result
+    // poisons the whole row (shaders/rkva/rkva_range_reduce_opt.hlsl:126-132)
+    if (a.poison && (bad || __builtin_amdgcn_ballot_w64(nonfin) != 0)) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) out[j] = NAN;
+        lse = NAN;
+    }
+    if (lane == 0 && a.lse) a.lse[row] = lse;
     const int iq = (int)((row % rows_per_seq) / a.H);
-    float* o = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1);
-    o[d] = out;
+    float* o = (float*)(a.dst + (int64_t)b * a.d_nb3 + (int64_t)iq * a.d_nb2 + (int64_t)h * a.d_nb1) + VPL * lane;
+    V ov;
+    float* oe = (float*)&ov;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) oe[j] = out[j];
+    *(V*)o = ov;
 }
 
 // Q rows -> image rows. One wave per (sequence, query, head) row.
@@ -886,10 +910,10 @@ hipError_t fa_reduce_launch(const FaArgs& a, int d, hipStream_t stream) {
     const int64_t n_rows = (int64_t)a.B * a.NQ * a.H;
     const bool wide = a.n_splits > 16;
     if (d == 128)
-        launch("fa_reduce", wide ? fa_reduce<128, 32> : fa_reduce<128, 16>, dim3((uint32_t)n_rows), dim3(128),
+        launch("fa_reduce", wide ? fa_reduce<128, 32> : fa_reduce<128, 16>, dim3((uint32_t)n_rows), dim3(64),
                stream, a);
     else
-        launch("fa_reduce", wide ? fa_reduce<256, 32> : fa_reduce<256, 16>, dim3((uint32_t)n_rows), dim3(256),
+        launch("fa_reduce", wide ? fa_reduce<256, 32> : fa_reduce<256, 16>, dim3((uint32_t)n_rows), dim3(64),
                stream, a);
     return hipGetLastError();
 }
