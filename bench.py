@@ -69,11 +69,14 @@ def make_fa_sets(torch, xq, wl, cfg, n_sets, seed=0):
         v = xq.DevTensor(cfg.kv_type, (D, L, Hkv, B), (wl.TYPE_SIZE[cfg.kv_type], Hkv * rec, rec, L * Hkv * rec), planes[1])
         qt = torch.randn((B, NQ, H, D), generator=gen, device="cuda", dtype=torch.float32)
         q = xq.DevTensor(wl.F32, (D, NQ, H, B), (4, H * D * 4, D * 4, NQ * H * D * 4), qt)
-        mt = torch.zeros((B, NQ, L), dtype=torch.float16, device="cuda")  # all-visible, one row per sequence
+        # one mask per sequence; rows past n_q (padding to n_q_pad) are all -inf
+        NP = cfg.n_q_pad or NQ
+        mt = torch.full((B, NP, L), float("-inf"), dtype=torch.float16, device="cuda")
+        mt[:, :NQ] = 0.0  # all visible
         if cfg.causal_prefix is not None:  # query i sees rows <= prefix + i
             for i in range(NQ):
                 mt[:, i, cfg.causal_prefix + i + 1:] = float("-inf")
-        m = xq.DevTensor(wl.F16, (L, NQ, 1, B), (2, L * 2, NQ * L * 2, NQ * L * 2), mt)
+        m = xq.DevTensor(wl.F16, (L, NP, 1, B), (2, L * 2, NP * L * 2, NP * L * 2), mt)
         dt = torch.empty((B, NQ, H, D), dtype=torch.float32, device="cuda")
         d = xq.DevTensor(wl.F32, (D, H, NQ, B), (4, D * 4, H * D * 4, NQ * H * D * 4), dt)
         sets.append((q, k, v, m, d))
@@ -124,9 +127,11 @@ def time_calls(torch, fn, n_sets, steps, warmup):
     return start.elapsed_time(stop) / steps  # ms per call
 
 
-def graph_time(torch, fn, n_sets, steps, warmup):
+def graph_time(torch, fn, n_sets, steps, warmup, stats=None):
     """ms per call: the n_sets calls captured once in a HIP graph, replayed until
-    `steps` calls ran (after `warmup` eager calls)."""
+    `steps` calls ran (after `warmup` eager calls). With a dict `stats`, also the
+    median, p10 and p90 of the per-call time over the replays (one replay = the
+    n_sets calls)."""
     for i in range(max(warmup, n_sets)):
         fn(i % n_sets)
     torch.cuda.synchronize()
@@ -139,13 +144,71 @@ def graph_time(torch, fn, n_sets, steps, warmup):
     graph.replay()
     torch.cuda.synchronize()
     reps = max(1, math.ceil(steps / n_sets))
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        graph.replay()
-    stop.record()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / (reps * n_sets), reps * n_sets
+    ev[0].record()
+    for r in range(reps):
+        graph.replay()
+        ev[r + 1].record()
+    torch.cuda.synchronize()
+    if stats is not None:
+        per = sorted(ev[r].elapsed_time(ev[r + 1]) / n_sets for r in range(reps))
+        stats.update(dist_ms(per))
+    return ev[0].elapsed_time(ev[reps]) / (reps * n_sets), reps * n_sets
+
+
+def quantile(sorted_vals, f):
+    """Linear-interpolated quantile of an ascending list."""
+    x = f * (len(sorted_vals) - 1)
+    i = int(math.floor(x))
+    j = min(i + 1, len(sorted_vals) - 1)
+    return sorted_vals[i] + (sorted_vals[j] - sorted_vals[i]) * (x - i)
+
+
+def dist_ms(sorted_ms):
+    """median / p10 / p90 in microseconds of ascending millisecond samples."""
+    return {"median_us": round(1000 * quantile(sorted_ms, 0.5), 3), "p10_us": round(1000 * quantile(sorted_ms, 0.1), 3),
+            "p90_us": round(1000 * quantile(sorted_ms, 0.9), 3), "samples": len(sorted_ms)}
+
+
+def kernel_samples(torch, xq, fn, n_sets, steps):
+    """Per call: each kernel's device duration (events the dispatch records),
+    one call at a time. Returns {kernel: ascending list of ms} and the list of
+    per-call sums."""
+    per_kernel, per_call = {}, []
+    for i in range(steps):
+        xq.profile_reset()
+        xq.profile_enable(True)
+        fn(i % n_sets)
+        torch.cuda.synchronize()
+        xq.profile_enable(False)
+        res = xq.profile_read()
+        tot = 0.0
+        for k, (ms, n) in res.items():
+            per_kernel.setdefault(k, []).append(ms)
+            tot += ms
+        per_call.append(tot)
+    xq.profile_reset()
+    return {k: sorted(v) for k, v in per_kernel.items()}, sorted(per_call)
+
+
+def host_info():
+    """nproc, the affinity mask and the CPU model of this host."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        aff = sorted(os.sched_getaffinity(0))
+        info["affinity_count"] = len(aff)
+        info["affinity"] = f"{aff[0]}-{aff[-1]}" if aff == list(range(aff[0], aff[-1] + 1)) else ",".join(map(str, aff))
+    except (AttributeError, OSError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return info
 
 
 def traffic_from_profiles(kernel, workload):
@@ -230,6 +293,8 @@ def cpu_fa_baseline(torch, wl, cfg, fa_set, threads, budget_s):
     host = lambda dt, t: wl.HostTensor(dt.type, dt.ne, dt.nb, t.t.reshape(-1).view(torch.uint8).cpu().numpy())
     hq, hk, hv, hm = host(q, q), host(k, k), host(v, v), host(m, m)
     hd = wl.HostTensor(wl.F32, d.ne, d.nb, np.zeros(d.t.numel() * 4, np.uint8))
+    oracle.flash_attn_ext(hq, hk, hv, hm, None, hd, cfg.kq_scale, 0.0, 0.0, oracle.QK_CONSISTENT, True,
+                          threads, want_lse=False)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
     while True:
@@ -252,6 +317,7 @@ def cpu_gdn_baseline(torch, wl, gdn_set, slots, threads, budget_s):
     import numpy as np
     import oracle
     hs = [wl.HostTensor(t.type, t.ne, t.nb, t.t.reshape(-1).view(torch.uint8).cpu().numpy()) for t in gdn_set]
+    oracle.gated_delta_net(*hs[:6], hs[6], slots, threads)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
     while True:
@@ -315,8 +381,11 @@ def main():
         log("calibration copy of 512 MiB done")
         del a, b
 
+    # int8 x int8 score dots and f16 x f16 value products on the matrix cores,
+    # softmax and every accumulation in f32
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "i8/f16 products, f32 accumulation", "data": "synthetic"}
 
     # ---------------- FA decode @32k q8_0 (headline)
     cfg = wl.FA_C2
@@ -335,8 +404,11 @@ def main():
             xq.flash_attn_ext(q, k, v, m, None, d, params, workspace=ws)
 
         log(f"FA: warmup {args.warmup}, timing {args.steps} calls (graph replays)")
-        ms_call, n_timed = graph_time(torch, fa_call, n_sets, args.steps, args.warmup)
+        call_stats = {}
+        ms_call, n_timed = graph_time(torch, fa_call, n_sets, args.steps, args.warmup, call_stats)
         kt = kernel_times(torch, xq, fa_call, n_sets, args.steps)
+        ks, pr = kernel_samples(torch, xq, fa_call, n_sets, args.steps)
+        pr_med = quantile(pr, 0.5) * 1e-3  # s, pass 1 + split merge per call
         gbs = alg / (ms_call * 1e-3) / 1e9
         k_us = kt.get("fa_dec", {}).get("avg_us", float("nan"))
         k_gbs = alg / (k_us * 1e-6) / 1e9
@@ -349,6 +421,7 @@ def main():
                        "n_seq": cfg.B, "mask": "f16 all-visible", "input_sets": n_sets, "timed_calls": n_timed,
                        "compute": "int8 MFMA q8_0 scores, f16 MFMA values, f32 online softmax and accumulation"},
             "us_per_call": round(ms_call * 1000, 2),
+            "call_us_dist": call_stats,
             "pct_of_8TBs": round(100 * gbs / PEAK_GBS, 1),
             "tokens_per_s_equiv": round(cfg.B * cfg.n_q / (ms_call * 1e-3), 1),
             "algorithmic_bytes": alg,
@@ -356,7 +429,13 @@ def main():
                          "unit": "GB/s", "frac": round(k_gbs / PEAK_GBS, 4),
                          "traffic": tr["traffic_bytes"] if tr else None,
                          "bytes_per_launch": alg, "avg_launch_us": round(k_us, 3)},
+            # the metric's pass 1 + split merge: both kernels' device durations per call
+            "pass1_reduce": {"median_us": round(pr_med * 1e6, 3), "p10_us": round(quantile(pr, 0.1) * 1000, 3),
+                             "p90_us": round(quantile(pr, 0.9) * 1000, 3), "samples": len(pr),
+                             "achieved_GB/s": round(alg / pr_med / 1e9, 1),
+                             "frac": round(alg / pr_med / 1e9 / PEAK_GBS, 4)},
             "kernels": kt,
+            "kernel_us_dist": {k: dist_ms(v) for k, v in ks.items()},
         })
 
     # ---------------- the other attention configs: f16 decode at 4k, q4_0 MTP verify
@@ -375,8 +454,10 @@ def main():
                 q, k, v, m, d = xsets[i]
                 xq.flash_attn_ext(q, k, v, m, None, d, xp, workspace=xws)
 
-            x_ms, x_n = graph_time(torch, x_call, x_sets_n, args.steps, args.warmup)
+            x_stats = {}
+            x_ms, x_n = graph_time(torch, x_call, x_sets_n, args.steps, args.warmup, x_stats)
             xkt = kernel_times(torch, xq, x_call, x_sets_n, args.steps)
+            xks, xpr = kernel_samples(torch, xq, x_call, x_sets_n, args.steps)
             x_alg = xcfg.algorithmic_bytes()
             x_kus = xkt.get("fa_dec", {}).get("avg_us", float("nan"))
             out[key] = {"workload": xcfg.name, "kv_type": {wl.F16: "f16", wl.Q4_0: "q4_0"}[xcfg.kv_type],
@@ -387,6 +468,8 @@ def main():
                         "fa_dec_GB/s": round(x_alg / (x_kus * 1e-6) / 1e9, 1),
                         "fa_dec_frac": round(x_alg / (x_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
                         "tokens_per_s_equiv": round(xcfg.B * xcfg.n_q / (x_ms * 1e-3), 1),
+                        "call_us_dist": x_stats, "pass1_reduce_us_dist": dist_ms(xpr),
+                        "kernel_us_dist": {k: dist_ms(v) for k, v in xks.items()},
                         "input_sets": x_sets_n, "timed_calls": x_n, "kernels": xkt}
             log(f"{key}: {x_ms * 1000:.2f} us/call, fa_dec {x_kus:.2f} us")
             del xsets, xws
@@ -401,8 +484,10 @@ def main():
         def gdn_call(i):
             xq.gated_delta_net(*gsets[i], gcfg.slots, mode=xq.GDN_STEP)
 
-        g_ms, _ = graph_time(torch, gdn_call, g_sets_n, max(args.steps, 100), args.warmup)
+        g_stats = {}
+        g_ms, _ = graph_time(torch, gdn_call, g_sets_n, max(args.steps, 100), args.warmup, g_stats)
         gkt = kernel_times(torch, xq, gdn_call, g_sets_n, max(args.steps, 100))
+        gks, _ = kernel_samples(torch, xq, gdn_call, g_sets_n, max(args.steps, 100))
         g_alg = gcfg.algorithmic_bytes()
         g_kus = gkt.get("gdn_step", {}).get("avg_us", float("nan"))
         log(f"GDN: {g_ms * 1000:.2f} us/call, kernel {g_kus:.2f} us")
@@ -416,7 +501,8 @@ def main():
                            "frac": round(g_alg / (g_kus * 1e-6) / 1e9 / PEAK_GBS, 4),
                            "call_GB/s": round(g_alg / (g_ms * 1e-3) / 1e9, 1),
                            "call_frac": round(g_alg / (g_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
-                           "traffic": g_tr["traffic_bytes"] if g_tr else None, "input_sets": g_sets_n}
+                           "traffic": g_tr["traffic_bytes"] if g_tr else None, "input_sets": g_sets_n,
+                           "call_us_dist": g_stats, "kernel_us_dist": {k: dist_ms(v) for k, v in gks.items()}}
         if args.only == "gdn":
             out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})
@@ -435,7 +521,8 @@ def main():
             xq.gated_delta_net(*psets[i], pcfg.slots, mode=xq.GDN_CHUNKED, workspace=p_ws)
 
         p_steps = max(args.steps // 2, 10)
-        p_ms, _ = graph_time(torch, prefill_call, p_sets_n, p_steps, args.warmup)
+        p_stats = {}
+        p_ms, _ = graph_time(torch, prefill_call, p_sets_n, p_steps, args.warmup, p_stats)
         pkt = kernel_times(torch, xq, prefill_call, p_sets_n, p_steps)
         p_alg = pcfg.algorithmic_bytes()
         log(f"GDN prefill: {p_ms * 1000:.2f} us/call; kernels {pkt}")
@@ -443,54 +530,68 @@ def main():
                               "algorithmic_bytes": p_alg, "call_GB/s": round(p_alg / (p_ms * 1e-3) / 1e9, 1),
                               "frac_of_hbm_roofline": round(p_alg / (p_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
                               "tokens_per_s": round(pcfg.T * pcfg.B / (p_ms * 1e-3), 1),
-                              "kernels": pkt, "workspace_bytes": int(p_ws.numel())}
+                              "call_us_dist": p_stats, "kernels": pkt, "workspace_bytes": int(p_ws.numel())}
         if args.only == "prefill":
             out.update({"value": round(p_alg / (p_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(p_ms, 5), "config": {"workload": pcfg.name}})
 
     # ---------------- CPU baselines (ggml-CPU semantics restated, this host's cores)
     if not args.no_cpu:
-        try:
-            threads = len(os.sched_getaffinity(0))
-        except AttributeError:
-            threads = os.cpu_count() or 1
-        threads = max(1, min(threads, 16))
+        host = host_info()
+        avail = host.get("affinity_count", os.cpu_count() or 1)
+        # one GPU's share of this pool's hosts is 16 cores (its job limits,
+        # OMP_NUM_THREADS / MAX_JOBS = 16): more threads than that would take
+        # cores from the other GPUs' jobs
+        threads = max(1, min(avail, 16))
+        host["threads_used"] = threads
+        host["thread_cap"] = "16 = one GPU's share of the host" if avail > 16 else None
+        runs = {}
         if args.only in ("fa", "all"):
             fa_call(0)
             torch.cuda.synchronize()
-            log(f"CPU baseline: FA on {threads} threads")
-            t_cpu, n_cpu, max_err = cpu_fa_baseline(torch, wl, cfg, sets[0], threads, args.cpu_budget)
+            for th in (threads, 1):
+                log(f"CPU baseline: FA on {th} threads")
+                runs[("fa", th)] = cpu_fa_baseline(torch, wl, cfg, sets[0], th, args.cpu_budget)
+            (t_cpu, n_cpu, max_err), (t1, n1, _) = runs[("fa", threads)], runs[("fa", 1)]
             out["cpu_baseline"] = {
                 "value": round(alg / t_cpu / 1e9, 3), "unit": "GB/s", "us_per_call": round(t_cpu * 1e6, 1),
                 "cores": threads, "kind": "port",
                 "sample": f"the full {cfg.name} call (same q8_0 bytes), oracle/xq_oracle.c ggml one-chunk "
-                          f"loop, median of {n_cpu} runs",
-                "gpu_vs_cpu_max_abs_err": max_err}
+                          f"loop (ggml-CPU semantics restated), median of {n_cpu} runs after one warm-up",
+                "one_thread": {"value": round(alg / t1 / 1e9, 3), "us_per_call": round(t1 * 1e6, 1),
+                               "median_of": n1},
+                "host": host, "gpu_vs_cpu_max_abs_err": max_err}
         if args.only in ("gdn", "all"):
             gdn_call(0)
             torch.cuda.synchronize()
-            log(f"CPU baseline: GDN on {threads} threads")
-            t_g, n_g, g_err = cpu_gdn_baseline(torch, wl, gsets[0], gcfg.slots, threads, args.cpu_budget / 2)
+            for th in (threads, 1):
+                log(f"CPU baseline: GDN on {th} threads")
+                runs[("gdn", th)] = cpu_gdn_baseline(torch, wl, gsets[0], gcfg.slots, th, args.cpu_budget / 2)
+            (t_g, n_g, g_err), (t_g1, n_g1, _) = runs[("gdn", threads)], runs[("gdn", 1)]
             gdn_cpu = {"us_per_call": round(t_g * 1e6, 1), "cores": threads, "kind": "port",
                        "GB/s": round(gcfg.algorithmic_bytes() / t_g / 1e9, 3), "median_of": n_g,
+                       "one_thread_us_per_call": round(t_g1 * 1e6, 1), "one_thread_median_of": n_g1,
                        "gpu_vs_cpu_max_abs_err": g_err}
             out["gdn_step"]["cpu_baseline"] = gdn_cpu
             if args.only == "gdn":
                 out["cpu_baseline"] = {"value": gdn_cpu["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
-                                       "sample": f"the full {gcfg.name} step, median of {n_g} runs"}
+                                       "sample": f"the full {gcfg.name} step, median of {n_g} runs", "host": host}
         if args.only in ("prefill", "all"):
             prefill_call(0)
             torch.cuda.synchronize()
-            log(f"CPU baseline: GDN prefill on {threads} threads")
-            t_p, n_p, p_err = cpu_gdn_baseline(torch, wl, psets[0], pcfg.slots, threads, args.cpu_budget / 4)
+            for th in (threads, 1):
+                log(f"CPU baseline: GDN prefill on {th} threads")
+                runs[("prefill", th)] = cpu_gdn_baseline(torch, wl, psets[0], pcfg.slots, th, args.cpu_budget / 4)
+            (t_p, n_p, p_err), (t_p1, n_p1, _) = runs[("prefill", threads)], runs[("prefill", 1)]
             p_cpu = {"us_per_call": round(t_p * 1e6, 1), "cores": threads, "kind": "port",
                      "GB/s": round(pcfg.algorithmic_bytes() / t_p / 1e9, 3), "median_of": n_p,
+                     "one_thread_us_per_call": round(t_p1 * 1e6, 1), "one_thread_median_of": n_p1,
                      "gpu_vs_cpu_max_abs_err": p_err}
             out["gdn_prefill"]["cpu_baseline"] = p_cpu
             if args.only == "prefill":
                 out["cpu_baseline"] = {"value": p_cpu["GB/s"], "unit": "GB/s", "cores": threads, "kind": "port",
                                        "sample": f"the full {pcfg.name} prefill (sequential recurrence), "
-                                                 f"median of {n_p} runs"}
+                                                 f"median of {n_p} runs", "host": host}
     else:
         out.setdefault("cpu_baseline", None)
     print(json.dumps(out), flush=True)
