@@ -341,6 +341,8 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
     ap.add_argument("--only", choices=["fa", "gdn", "prefill", "all"], default="all")
+    ap.add_argument("--copy-ceiling", action="store_true",
+                    help="also time a plain device copy of the GDN step's bytes (its practical ceiling)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary of --pmc-kernel from two rocprofv3 --pmc output dirs and exit")
     ap.add_argument("--pmc-kernel", choices=["fa_dec", "gdn_step"], default="fa_dec",
@@ -503,6 +505,42 @@ def main():
                            "call_frac": round(g_alg / (g_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
                            "traffic": g_tr["traffic_bytes"] if g_tr else None, "input_sets": g_sets_n,
                            "call_us_dist": g_stats, "kernel_us_dist": {k: dist_ms(v) for k, v in gks.items()}}
+        if args.copy_ceiling:
+            # the step moves the state in (17 MB) and out (17 MB) plus 0.4 MB of token
+            # inputs and outputs: a device copy of half the algorithmic bytes reads
+            # and writes the same amount, on the same rotation of distinct buffers
+            half = g_alg // 2
+            bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda"),
+                     torch.empty(half, dtype=torch.uint8, device="cuda")) for _ in range(g_sets_n)]
+
+            fbufs = [(a.view(torch.float32), b.view(torch.float32)) for a, b in bufs]
+
+            def copy_call(i):  # the runtime's device-to-device copy
+                bufs[i][1].copy_(bufs[i][0])
+
+            def ew_call(i):  # an elementwise kernel reading and writing the same bytes
+                torch.mul(fbufs[i][0], 1.0, out=fbufs[i][1])
+
+            import ctypes
+            probe = ctypes.CDLL(str(ROOT / "xllama-qwen35-xbox_amd" / "xqattn" / "libxqprobe.so"))
+            probe.xqp_stream_copy.restype = ctypes.c_int
+            probe.xqp_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+            half16 = half // 16 * 16
+
+            def stream_call(i):  # a streaming copy with the step kernel's launch shape
+                st = probe.xqp_stream_copy(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), half16,
+                                           torch.cuda.current_stream().cuda_stream)
+                assert st == 0, st
+
+            ceil = {"bytes": 2 * half}
+            for name, fn in (("memcpy", copy_call), ("elementwise", ew_call), ("stream_copy", stream_call)):
+                c_stats = {}
+                c_ms, _ = graph_time(torch, fn, g_sets_n, max(args.steps, 100), args.warmup, c_stats)
+                ceil[name] = {"us_per_call": round(c_ms * 1000, 3), "GB/s": round(2 * half / (c_ms * 1e-3) / 1e9, 1),
+                              "call_us_dist": c_stats}
+                log(f"copy ceiling ({name}): {c_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
+            out["gdn_step"]["copy_ceiling"] = ceil
+            del bufs, fbufs
         if args.only == "gdn":
             out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})
