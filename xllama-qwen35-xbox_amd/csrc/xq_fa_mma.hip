@@ -630,9 +630,10 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     //      pw: f32 weights (row 4lg + i, pair 16m + lr; quantized V: times
     //      2^S_p); seenm: careful slice's masks of the rows the pair sees;
     //      Bf: F16/E5M2 weight operands; vsan: V sanitising
-    auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], bool careful, const uint32_t (&seenm)[MT][2],
+    auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], auto careful_tag, const uint32_t (&seenm)[MT][2],
                       const h8 (&Bf)[MT], bool vsan) {
         constexpr int ST = decltype(st_tag)::value;
+        constexpr bool careful = decltype(careful_tag)::value;  // a separate copy: no mask selects when false
         const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
         uint32_t X[4];
 #pragma unroll
@@ -662,7 +663,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     wd_f16<true>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
                 else
                     wd_f16<false>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
-                if (careful) {  // rows the pair does not see add 0, whatever their scale holds
+                if constexpr (careful) {  // rows the pair does not see add 0, whatever their scale holds
                     b01 &= seenm[m][0];
                     b23 &= seenm[m][1];
                 }
@@ -727,19 +728,18 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // without a partner while the workgroup waits for them. Each wave posts its
     // progress and takes issue priority while it is behind its partner (ties go
     // to the younger wave).
-    // quantized V: pair p's accumulators hold sum w * 2^S_p * d_v * q, with
+    // quantized V: pair p's accumulators hold sum w * 2^S_p * d_v * q and its
+    // weight sum sum w * 2^S_p (the weights are formed as exp2(x - mu + S_p)), with
     // S_p = 25 - the largest block-scale exponent field among the rows p has
     // seen so far (so w * 2^S_p * |d_v| < 2^15). S_p depends on p's rows only,
     // so a pair's bits do not depend on the pairs that share its tile; it only
-    // falls, and every fall rescales p's accumulator column by a power of two.
+    // falls, and every fall rescales p's accumulator column and sum by a power of two.
     int e_max[MT], s_exp[MT];
-    float wscale[MT];
     int e_min = -1;  // wave-uniform: the smallest e_max over the pairs (-1 while one has seen no row)
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         e_max[m] = -1;
         s_exp[m] = 0;
-        wscale[m] = 1.0f;
     }
     int done = 0;
     if (lane == 0) sProg[wave] = 0;
@@ -834,7 +834,9 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const float mt = xrow_max(fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3])));
-            mnew[m] = mt > m_run[m] + kLazyMax ? mt : m_run[m];
+            // integer maxima: every rescale factor is an exact power of two and
+            // the pair's power 2^S_p folds exactly into the exponent argument
+            mnew[m] = mt > m_run[m] + kLazyMax ? ceilf(mt) : m_run[m];
             grow |= mnew[m] != m_run[m];
         }
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -845,22 +847,6 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
                 for (int n = 0; n < 2 * NB; ++n) acc[m][n] *= al;
                 m_run[m] = mnew[m];
-            }
-        }
-        float pw[MT][4];
-        h8 Bf[MT];  // F16/E5M2 V: weights as f16 high parts (products 0..3), low parts (4..7)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const float mu = m_run[m] == -INFINITY ? 0.0f : m_run[m] + kPOff;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pw[m][i] = __builtin_amdgcn_exp2f(x[m][i] - mu);
-            l_run[m] += (pw[m][0] + pw[m][1]) + (pw[m][2] + pw[m][3]);
-            if constexpr (!QUANT) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    Bf[m][i] = (_Float16)pw[m][i];
-                    Bf[m][4 + i] = (_Float16)(pw[m][i] - (float)Bf[m][i]);
-                }
             }
         }
         // -- quantized V: each pair's largest block-scale exponent over the rows
@@ -909,8 +895,8 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                         const float f = __builtin_ldexpf(1.0f, s_new - s_exp[m]);  // exact power of two
 #pragma unroll
                         for (int n = 0; n < 2 * NB; ++n) acc[m][n] *= f;
+                        l_run[m] *= f;
                         s_exp[m] = s_new;
-                        wscale[m] = __builtin_ldexpf(1.0f, s_new);
                         e_max[m] = grow ? ep[m] : e_max[m];
                     }
                     emn = min(emn, e_max[m]);
@@ -933,10 +919,22 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     seenmask[m][1] = (x[m][2] != -INFINITY ? 0xffffu : 0u) | (x[m][3] != -INFINITY ? 0xffff0000u : 0u);
                 }
             }
+        }
+        float pw[MT][4];
+        h8 Bf[MT];  // F16/E5M2 V: weights as f16 high parts (products 0..3), low parts (4..7)
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
+        for (int m = 0; m < MT; ++m) {
+            // quantized V: weights times 2^S_p (exact: integer maximum, integer S_p)
+            const float mu = (m_run[m] == -INFINITY ? 0.0f : m_run[m] + kPOff) - (QUANT ? (float)s_exp[m] : 0.0f);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) pw[m][i] *= wscale[m];
+            for (int i = 0; i < 4; ++i) pw[m][i] = __builtin_amdgcn_exp2f(x[m][i] - mu);
+            l_run[m] += (pw[m][0] + pw[m][1]) + (pw[m][2] + pw[m][3]);
+            if constexpr (!QUANT) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    Bf[m][i] = (_Float16)pw[m][i];
+                    Bf[m][4 + i] = (_Float16)(pw[m][i] - (float)Bf[m][i]);
+                }
             }
         }
         // -- careful F16/E5M2 slice: a non-finite V element must not reach the
@@ -976,8 +974,18 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 }
             }
         }
+        if constexpr (QUANT) {
+            if (careful) {
 #pragma unroll
-        for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, careful, seenmask, Bf, vsan);
+                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::true_type{}, seenmask, Bf, vsan);
+            } else {
+#pragma unroll
+                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::false_type{}, seenmask, Bf, vsan);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::false_type{}, seenmask, Bf, vsan);
+        }
 
         // -- the V unit of slice j+2 into the stage this slice's V used
         if (n2) {
@@ -1003,13 +1011,14 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     float* mb = (float*)smem;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const float lt = xrow_sum(l_run[m]);
+        // quantized V: l and the accumulators hold 2^S_p times their values (exact)
+        const float unscale = __builtin_ldexpf(1.0f, -s_exp[m]);
+        const float lt = xrow_sum(QUANT ? l_run[m] * unscale : l_run[m]);
         if (lg == 0) {
             sM[wave][16 * m + lr] = m_run[m] == -INFINITY ? -INFINITY : m_run[m] + kPOff;
             sL[wave][16 * m + lr] = lt;
         }
         float* mw = mb + (wave * 16 + lr) * MS;
-        const float unscale = __builtin_ldexpf(1.0f, -s_exp[m]);  // quantized V: undo 2^S_p (exact)
         // the lane's dims of block c as 16-byte writes (acc_dim's layout);
         // padding pairs are never read
         if (16 * m + lr < npa) {
