@@ -15,8 +15,8 @@ repeats. Reported:
                HIP-graph replays of calls on rotated input sets;
   roofline     the dominant kernel (fa_dec, the whole call in one launch):
                algorithmic bytes of one launch / its average device duration
-               from HIP events recorded around each launch on the stream it is
-               launched on; peak 8 TB/s; traffic = HBM bytes per launch from
+               from HIP events its dispatch records on the stream it is launched
+               on, one call at a time; peak 8 TB/s; traffic = HBM bytes per launch from
                the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
                (profiles/, scaled by the same counters on a plain copy), else null;
   cpu_baseline the ggml-CPU restatement (oracle/, "port") on the host cores of
@@ -129,9 +129,9 @@ def time_calls(torch, fn, n_sets, steps, warmup):
 
 def graph_time(torch, fn, n_sets, steps, warmup, stats=None):
     """ms per call: the n_sets calls captured once in a HIP graph, replayed until
-    `steps` calls ran (after `warmup` eager calls). With a dict `stats`, also the
-    median, p10 and p90 of the per-call time over the replays (one replay = the
-    n_sets calls)."""
+    `steps` calls ran (after `warmup` eager calls), timed as one span. With a dict
+    `stats`, also the median, p10 and p90 of the per-call time over blocks of
+    replays in a second pass (one replay = the n_sets calls)."""
     for i in range(max(warmup, n_sets)):
         fn(i % n_sets)
     torch.cuda.synchronize()
@@ -144,17 +144,30 @@ def graph_time(torch, fn, n_sets, steps, warmup, stats=None):
     graph.replay()
     torch.cuda.synchronize()
     reps = max(1, math.ceil(steps / n_sets))
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    # the timed region: the replays back to back between one event pair
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    ev[0].record()
+    t0.record()
     for r in range(reps):
         graph.replay()
-        ev[r + 1].record()
+    t1.record()
     torch.cuda.synchronize()
     if stats is not None:
-        per = sorted(ev[r].elapsed_time(ev[r + 1]) / n_sets for r in range(reps))
+        # the spread, from a second pass: one sample per block of BLOCK replays
+        # (an event between replays costs several microseconds of its own, which
+        # a block spreads over its calls; this pass does not set the mean)
+        BLOCK = 4
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for r in range(reps):
+            for _ in range(BLOCK):
+                graph.replay()
+            ev[r + 1].record()
+        torch.cuda.synchronize()
+        per = sorted(ev[r].elapsed_time(ev[r + 1]) / (BLOCK * n_sets) for r in range(reps))
         stats.update(dist_ms(per))
-    return ev[0].elapsed_time(ev[reps]) / (reps * n_sets), reps * n_sets
+        stats["calls_per_sample"] = BLOCK * n_sets
+    return t0.elapsed_time(t1) / (reps * n_sets), reps * n_sets
 
 
 def quantile(sorted_vals, f):
@@ -412,7 +425,11 @@ def main():
         ks, pr = kernel_samples(torch, xq, fa_call, n_sets, args.steps)
         pr_med = quantile(pr, 0.5) * 1e-3  # s, pass 1 + split merge per call
         gbs = alg / (ms_call * 1e-3) / 1e9
-        k_us = kt.get("fa_dec", {}).get("avg_us", float("nan"))
+        # fa_dec's average device duration from the events its dispatch records,
+        # one call at a time: in the graph replays the launches run back to back
+        # at this duration (rocprofv3 sees no gap between them), while the eager
+        # back-to-back pass (`kernels`) leaves the host's launch gaps between them
+        k_us = 1000 * statistics.fmean(ks["fa_dec"]) if "fa_dec" in ks else float("nan")
         k_gbs = alg / (k_us * 1e-6) / 1e9
         log(f"FA: {ms_call * 1000:.2f} us/call, {gbs:.0f} GB/s; kernels {kt}")
         tr = traffic_from_profiles("fa_dec", cfg.name)
