@@ -141,12 +141,24 @@ def graph_time(torch, fn, n_sets, steps, warmup, stats=None):
     with torch.cuda.graph(graph, stream=stream):
         for i in range(n_sets):
             fn(i)
-    graph.replay()
+    # untimed warm-up replays, at least 20 ms of them: right after the capture
+    # (and after the host's idle time) the first replays run slower
+    t_warm = time.perf_counter()
+    n_warm = 0
+    while n_warm < max(2, math.ceil(warmup / n_sets)) or time.perf_counter() - t_warm < 0.02:
+        graph.replay()
+        n_warm += 1
+        if n_warm % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     reps = max(1, math.ceil(steps / n_sets))
-    # the timed region: the replays back to back between one event pair
+    # the timed region: the replays back to back between one event pair. One
+    # untimed replay is queued ahead of the start event, so the GPU is busy
+    # while the host submits the timed replays (started from an idle GPU, the
+    # span would also hold the host's submission of the first ones)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    graph.replay()
     t0.record()
     for r in range(reps):
         graph.replay()
@@ -158,6 +170,7 @@ def graph_time(torch, fn, n_sets, steps, warmup, stats=None):
         # a block spreads over its calls; this pass does not set the mean)
         BLOCK = 4
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        graph.replay()
         ev[0].record()
         for r in range(reps):
             for _ in range(BLOCK):
