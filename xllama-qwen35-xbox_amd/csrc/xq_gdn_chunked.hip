@@ -18,7 +18,8 @@
 // Two kernels:
 //   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
 //                   parallel: K K^T on f16 MFMA (f32 accumulation) and the unit
-//                   lower-triangular solve for T in f32; stores T as f16 hi + lo
+//                   lower-triangular inverse for T in f32 (by 16 x 16 blocks,
+//                   the products on f32 MFMA); stores T as f16 hi + lo
 //                   planes, the decay vectors, the cumulative log-decays G and
 //                   the chunk's largest |v| per 16-column block (17 KB per
 //                   chunk) in the workspace. f32 k rows enter as f16 hi + lo
@@ -280,45 +281,75 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         sKK[t * FP + j] = L;
     }
     __syncthreads();
-    // ---- T = (I + L)^{-1} diag(beta): column j by a quad of lanes; lane part p
-    //      keeps x_s for s in [16p, 16p + 16) and the quad sums the dot products
-    //      (four partial chains per lane). Row t of L (the lane's 16 values,
-    //      four 16-byte reads) is loaded two steps ahead: the loop is a chain of
-    //      64 dependent steps, and a read issued in its own step would put the
-    //      LDS latency into every one of them.
-    float* sT = (float*)sK;  // T [t][j], f32
+    // ---- M = (I + L)^{-1} by blocks of 16 (T = M diag(beta) is formed at the
+    //      record). With D_i = I + L_ii the unit lower-triangular diagonal blocks:
+    //        1. M_ii = D_i^{-1}, one wave per block, a 16-step substitution;
+    //        2. the 32 x 32 diagonal blocks: M_10 = -M_11 L_10 M_00 and
+    //           M_32 = -M_33 L_32 M_22;
+    //        3. the lower-left 32 x 32 block: -M_B C M_A with C = L[32..64)[0..32)
+    //           and M_A, M_B the 32 x 32 inverses of step 2.
+    //      The products run on f32 MFMA. The dependent chain is 16 substitution
+    //      steps and six 16 x 16 x 16 products, against 64 steps for a column-wise
+    //      substitution. The upper-triangular blocks of L (zero, never read
+    //      again) hold the intermediate products.
+    float* sT = (float*)sK;  // M [t][j], f32
+    auto blk = [&](float* base, int bi, int bj) { return base + 16 * bi * FP + 16 * bj; };
+    // acc += A B for 16 x 16 blocks A, B (row stride FP), on f32 MFMA
+    auto mm16 = [&](const float* A, const float* B, f4 acc) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[lr * FP + 4 * kb + lg], B[(4 * kb + lg) * FP + lr], acc, 0, 0, 0);
+        return acc;
+    };
+    auto st16 = [&](float* C, const f4& v, float sgn) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) C[(4 * lg + r) * FP + lr] = sgn * v[r];
+    };
     {
-        const int j = wave * 16 + (lane >> 2), p = lane & 3;
-        float x[16];
+        // 1. D_w^{-1}: column c by a quad of lanes, lane part p keeps rows 4p..4p+3
+        //    and the quad sums the dot products; the rows of L are read two
+        //    steps ahead so the LDS latency stays off the chain
+        const int c = lane >> 2, p = lane & 3, o = 16 * wave;
+        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        f4 Lq[3];
+        auto ldrow = [&](int t) { return *(const f4*)(sKK + (o + t) * FP + o + 4 * p); };
+        Lq[1] = ldrow(1);
+        Lq[2] = ldrow(2);
 #pragma unroll
-        for (int m = 0; m < 16; ++m) x[m] = 0.0f;
-        const float bj = sBeta[j];
-        f4 Lq[3][4];  // rows t, t + 1, t + 2 (ring by t % 3)
-        auto ldrow = [&](int t, f4 (&r)[4]) {
-            const f4* Lr = (const f4*)(sKK + t * FP + 16 * p);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) r[u] = Lr[u];
-        };
-        ldrow(1, Lq[1]);
-        ldrow(2, Lq[2]);
-#pragma unroll
-        for (int t = 0; t < 64; ++t) {
+        for (int t = 0; t < 16; ++t) {
             float part = 0.0f;
             if (t > 0) {
-                if (t + 2 < 64) ldrow(t + 2, Lq[(t + 2) % 3]);
-                const f4 (&Lr)[4] = Lq[t % 3];
-                float c4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int m = 0; m < 16; ++m) c4[m & 3] = fmaf(Lr[m >> 2][m & 3], x[m], c4[m & 3]);  // L[t][s >= t] = 0
-                part = (c4[0] + c4[1]) + (c4[2] + c4[3]);
+                if (t + 2 < 16) Lq[(t + 2) % 3] = ldrow(t + 2);
+                const f4 Lr = Lq[t % 3];  // L[t][s >= t] = 0
+                part = fmaf(Lr[1], x[1], Lr[0] * x[0]) + fmaf(Lr[3], x[3], Lr[2] * x[2]);
             }
             part += dpp<0xB1>(part);  // quad: lanes p ^ 1
             part += dpp<0x4E>(part);  // quad: lanes p ^ 2
-            const float xt = t < j ? 0.0f : (t == j ? bj : -part);
-            if ((t >> 4) == p) x[t & 15] = xt;
+            const float xt = t < c ? 0.0f : (t == c ? 1.0f : -part);
+            if ((t >> 2) == p) x[t & 3] = xt;
         }
 #pragma unroll
-        for (int m = 0; m < 16; ++m) sT[(16 * p + m) * FP + j] = x[m];
+        for (int m = 0; m < 4; ++m) sT[(o + 4 * p + m) * FP + o + c] = x[m];
+        // the upper-triangular blocks of M are zero
+        for (int bj = wave + 1; bj < 4; ++bj) st16(blk(sT, wave, bj), f4{0.0f, 0.0f, 0.0f, 0.0f}, 1.0f);
+    }
+    __syncthreads();
+    if (wave < 2) {  // 2. wave 0: M_10, wave 1: M_32 (scratch: L blocks (0, 1), (2, 3))
+        const int i = 2 * wave + 1, j = 2 * wave;
+        float* P = blk(sKK, j, i);
+        st16(P, mm16(blk(sKK, i, j), blk(sT, j, j), f4{0.0f, 0.0f, 0.0f, 0.0f}), 1.0f);
+        st16(blk(sT, i, j), mm16(blk(sT, i, i), P, f4{0.0f, 0.0f, 0.0f, 0.0f}), -1.0f);
+    }
+    __syncthreads();
+    {  // 3. wave w: block (i, j) = (2 + w / 2, w % 2); Q = C M_A in L blocks (j, i)
+        const int i = 2 + (wave >> 1), j = wave & 1;
+        f4 q = mm16(blk(sKK, i, 1), blk(sT, 1, j), f4{0.0f, 0.0f, 0.0f, 0.0f});
+        if (j == 0) q = mm16(blk(sKK, i, 0), blk(sT, 0, 0), q);
+        st16(blk(sKK, j, i), q, 1.0f);
+        __syncthreads();
+        f4 r = mm16(blk(sT, i, 2), blk(sKK, j, 2), f4{0.0f, 0.0f, 0.0f, 0.0f});
+        if (i == 3) r = mm16(blk(sT, 3, 3), blk(sKK, j, 3), r);
+        st16(blk(sT, i, j), r, -1.0f);
     }
     __syncthreads();
 
@@ -329,7 +360,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         h8 th[2], tl[2];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const float tv = sT[t * FP + j0 + e];
+            const float tv = sT[t * FP + j0 + e] * sBeta[j0 + e];  // T = M diag(beta)
             th[e >> 3][e & 7] = f16_hi(tv), tl[e >> 3][e & 7] = f16_lo(tv);
         }
         const int o = (t * 64 + j0) * 2;
