@@ -16,8 +16,9 @@
 // which equals the token-by-token recurrence in exact arithmetic.
 //
 // Two kernels:
-//   gdn_chunk_prep  one workgroup per (sequence, v-head, chunk), all chunks in
-//                   parallel: K K^T on f16 MFMA (f32 accumulation) and the unit
+//   gdn_chunk_prep  one workgroup per (sequence, k-head, chunk), all chunks in
+//                   parallel, for the two v-heads that share the k-head: K K^T on
+//                   f16 MFMA once (f32 accumulation) and, per v-head, the unit
 //                   lower-triangular inverse for T in f32 (by 16 x 16 blocks,
 //                   the products on f32 MFMA); stores T as f16 hi + lo
 //                   planes, the decay vectors, the cumulative log-decays G and
@@ -183,18 +184,18 @@ template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs a) {
     constexpr int KP = 136;  // padded f16 row stride (halves)
     constexpr int FP = 68;   // padded f32 row stride (16-byte rows, conflict-free MFMA stores)
-    // 35 KB for bf16 rows (52 KB for f32 rows); after the products sK becomes T.
-    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then T f32 [64][FP]
-    __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // K K^T, then L
-    __shared__ float sG[64], sBeta[64], sEG[64];
-    __shared__ uint32_t sVmax[kColBlocks];  // bits of the largest |v| per column block
+    // 36 KB for bf16 rows (53 KB for f32 rows); after the products sK becomes M.
+    __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then M f32 [64][FP]
+    __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // L of one v-head
+    __shared__ float sG[2][64], sBeta[2][64], sEG[2][64];
+    __shared__ uint32_t sVmax[2][kColBlocks];  // bits of the largest |v| per column block
     // f32 rows: the f16 remainders of K
     constexpr int NKL = BF16 ? 8 : 64 * KP;
     __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
     static_assert(64 * FP * 4 <= 64 * KP * 2, "LDS aliases");
 
-    const int n = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int kh = h % 16;
+    // v-heads kh and kh + 16 share k-head kh: K K^T is formed once for both
+    const int n = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
     const int t0 = n * kChunk;
@@ -220,69 +221,72 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             *(h8*)(sK + t * KP + i0) = hk;
             if constexpr (!BF16) *(h8*)(sKl + t * KP + i0) = lo_h8(xk, hk);
         }
-        // largest |v| of the token's 32 columns 32qt.. (two column blocks); a
-        // NaN compares as the largest bits, so it reaches the scan's choice
-        if (tid < kColBlocks) sVmax[tid] = 0;
-        uint32_t vm[2] = {0, 0};
+        // largest |v| of the token's 32 columns 32qt.. (two column blocks) for
+        // each v-head; a NaN compares as the largest bits, so it reaches the
+        // scan's choice
+        if (tid < 2 * kColBlocks) sVmax[tid / kColBlocks][tid % kColBlocks] = 0;
+        uint32_t vm[2][2] = {{0, 0}, {0, 0}};
         if (ok) {
-            const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tg * a.v_nb2 + (int64_t)h * a.v_nb1;
 #pragma unroll
-            for (int gi = 0; gi < 4; ++gi) {
-                float xv[8];
-                load8<BF16, false>(vr, 32 * qt + 8 * gi, xv);
+            for (int e2 = 0; e2 < 2; ++e2) {
+                const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tg * a.v_nb2 + (int64_t)(kh + 16 * e2) * a.v_nb1;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vm[gi >> 1] = max(vm[gi >> 1], __float_as_uint(xv[e]) & 0x7fffffffu);
+                for (int gi = 0; gi < 4; ++gi) {
+                    float xv[8];
+                    load8<BF16, false>(vr, 32 * qt + 8 * gi, xv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        vm[e2][gi >> 1] = max(vm[e2][gi >> 1], __float_as_uint(xv[e]) & 0x7fffffffu);
+                }
             }
         }
         __syncthreads();  // sVmax cleared
-        atomicMax(&sVmax[2 * qt], vm[0]);
-        atomicMax(&sVmax[2 * qt + 1], vm[1]);
-        if (tid < 64) {
-            const int tt = t0 + tid;
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+            atomicMax(&sVmax[e2][2 * qt], vm[e2][0]);
+            atomicMax(&sVmax[e2][2 * qt + 1], vm[e2][1]);
+        }
+        if (tid < 128) {
+            const int e2 = tid >> 6, tt = t0 + (tid & 63), h = kh + 16 * e2;
             const bool ok2 = tt < a.T;
-            sG[tid] = ok2 ? *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)tt * a.g_nb2 + (int64_t)h * a.g_nb1) : 0.0f;
-            sBeta[tid] = ok2 ? *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)tt * a.b_nb2 + (int64_t)h * a.b_nb1) : 0.0f;
+            sG[e2][tid & 63] = ok2 ? *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)tt * a.g_nb2 + (int64_t)h * a.g_nb1) : 0.0f;
+            sBeta[e2][tid & 63] = ok2 ? *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)tt * a.b_nb2 + (int64_t)h * a.b_nb1) : 0.0f;
         }
     }
     __syncthreads();
-    // cumulative log-decay (sequential sum, as the recurrence applies the decays)
-    if (tid < 64) {
+    // cumulative log-decays (sequential sums, as the recurrence applies the decays)
+    if (tid < 128) {
+        const int e2 = tid >> 6, t = tid & 63;
         float G = 0.0f;
-        for (int s = 0; s <= tid; ++s) G += sG[s];
-        sEG[tid] = G;
+        for (int s = 0; s <= t; ++s) G += sG[e2][s];
+        sEG[e2][t] = G;
     }
-    // ---- K K^T: 16 tiles, 4 per wave, contraction over 128 key dims
+    // ---- K K^T: 16 tiles, 4 per wave, contraction over 128 key dims; kept in
+    //      registers for the L of both v-heads
+    f4 kk[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
         const int tile = wave * 4 + tt;
         const int mt = tile >> 2, nt = tile & 3;
-        f4 kk = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        kk[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 bk = *(const h8*)(sK + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
             const h8 ak = *(const h8*)(sK + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
-            kk = mfma32(ak, bk, kk);
+            kk[tt] = mfma32(ak, bk, kk[tt]);
             if constexpr (!BF16) {
                 const h8 bkl = *(const h8*)(sKl + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
                 const h8 akl = *(const h8*)(sKl + (mt * 16 + lr) * KP + ks * 32 + 8 * lg);
-                kk = mfma32(ak, bkl, kk);
-                kk = mfma32(akl, bk, kk);
+                kk[tt] = mfma32(ak, bkl, kk[tt]);
+                kk[tt] = mfma32(akl, bk, kk[tt]);
             }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sKK[(mt * 16 + 4 * lg + r) * FP + nt * 16 + lr] = kk[r];
     }
     __syncthreads();  // K no longer read; G ready
-    // ---- L (strictly lower, in place of K K^T)
-#pragma unroll 4
-    for (int e = tid; e < 64 * 64; e += 256) {
-        const int t = e >> 6, j = e & 63;
-        const float L = j < t ? sBeta[t] * __expf(sEG[t] - sEG[j]) * sKK[t * FP + j] : 0.0f;
-        sKK[t * FP + j] = L;
-    }
-    __syncthreads();
-    // ---- M = (I + L)^{-1} by blocks of 16 (T = M diag(beta) is formed at the
-    //      record). With D_i = I + L_ii the unit lower-triangular diagonal blocks:
+
+    // ---- per v-head: M = (I + L)^{-1} by blocks of 16 (T = M diag(beta) is
+    //      formed at the record). With D_i = I + L_ii the unit lower-triangular
+    //      diagonal blocks:
     //        1. M_ii = D_i^{-1}, one wave per block, a 16-step substitution;
     //        2. the 32 x 32 diagonal blocks: M_10 = -M_11 L_10 M_00 and
     //           M_32 = -M_33 L_32 M_22;
@@ -305,80 +309,98 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
 #pragma unroll
         for (int r = 0; r < 4; ++r) C[(4 * lg + r) * FP + lr] = sgn * v[r];
     };
-    {
-        // 1. D_w^{-1}: column c by a quad of lanes, lane part p keeps rows 4p..4p+3
-        //    and the quad sums the dot products; the rows of L are read two
-        //    steps ahead so the LDS latency stays off the chain
-        const int c = lane >> 2, p = lane & 3, o = 16 * wave;
-        float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        f4 Lq[3];
-        auto ldrow = [&](int t) { return *(const f4*)(sKK + (o + t) * FP + o + 4 * p); };
-        Lq[1] = ldrow(1);
-        Lq[2] = ldrow(2);
+    for (int e2 = 0; e2 < 2; ++e2) {
+        const int h = kh + 16 * e2;
+        // L (strictly lower) from the K K^T tiles. The previous v-head's last
+        // reads of sKK sit before the barrier that ends its inverse, its reads
+        // of M before the barrier below.
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            float part = 0.0f;
-            if (t > 0) {
-                if (t + 2 < 16) Lq[(t + 2) % 3] = ldrow(t + 2);
-                const f4 Lr = Lq[t % 3];  // L[t][s >= t] = 0
-                part = fmaf(Lr[1], x[1], Lr[0] * x[0]) + fmaf(Lr[3], x[3], Lr[2] * x[2]);
+        for (int tt = 0; tt < 4; ++tt) {
+            const int tile = wave * 4 + tt;
+            const int mt = tile >> 2, nt = tile & 3;
+            const int j = nt * 16 + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = mt * 16 + 4 * lg + r;
+                sKK[t * FP + j] = j < t ? sBeta[e2][t] * __expf(sEG[e2][t] - sEG[e2][j]) * kk[tt][r] : 0.0f;
             }
-            part += dpp<0xB1>(part);  // quad: lanes p ^ 1
-            part += dpp<0x4E>(part);  // quad: lanes p ^ 2
-            const float xt = t < c ? 0.0f : (t == c ? 1.0f : -part);
-            if ((t >> 2) == p) x[t & 3] = xt;
         }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) sT[(o + 4 * p + m) * FP + o + c] = x[m];
-        // the upper-triangular blocks of M are zero
-        for (int bj = wave + 1; bj < 4; ++bj) st16(blk(sT, wave, bj), f4{0.0f, 0.0f, 0.0f, 0.0f}, 1.0f);
-    }
-    __syncthreads();
-    if (wave < 2) {  // 2. wave 0: M_10, wave 1: M_32 (scratch: L blocks (0, 1), (2, 3))
-        const int i = 2 * wave + 1, j = 2 * wave;
-        float* P = blk(sKK, j, i);
-        st16(P, mm16(blk(sKK, i, j), blk(sT, j, j), f4{0.0f, 0.0f, 0.0f, 0.0f}), 1.0f);
-        st16(blk(sT, i, j), mm16(blk(sT, i, i), P, f4{0.0f, 0.0f, 0.0f, 0.0f}), -1.0f);
-    }
-    __syncthreads();
-    {  // 3. wave w: block (i, j) = (2 + w / 2, w % 2); Q = C M_A in L blocks (j, i)
-        const int i = 2 + (wave >> 1), j = wave & 1;
-        f4 q = mm16(blk(sKK, i, 1), blk(sT, 1, j), f4{0.0f, 0.0f, 0.0f, 0.0f});
-        if (j == 0) q = mm16(blk(sKK, i, 0), blk(sT, 0, 0), q);
-        st16(blk(sKK, j, i), q, 1.0f);
         __syncthreads();
-        f4 r = mm16(blk(sT, i, 2), blk(sKK, j, 2), f4{0.0f, 0.0f, 0.0f, 0.0f});
-        if (i == 3) r = mm16(blk(sT, 3, 3), blk(sKK, j, 3), r);
-        st16(blk(sT, i, j), r, -1.0f);
-    }
-    __syncthreads();
+        {
+            // 1. D_w^{-1}: column c by a quad of lanes, lane part p keeps rows
+            //    4p..4p+3 and the quad sums the dot products; the rows of L are
+            //    read two steps ahead so the LDS latency stays off the chain
+            const int c = lane >> 2, p = lane & 3, o = 16 * wave;
+            float x[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            f4 Lq[3];
+            auto ldrow = [&](int t) { return *(const f4*)(sKK + (o + t) * FP + o + 4 * p); };
+            Lq[1] = ldrow(1);
+            Lq[2] = ldrow(2);
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                float part = 0.0f;
+                if (t > 0) {
+                    if (t + 2 < 16) Lq[(t + 2) % 3] = ldrow(t + 2);
+                    const f4 Lr = Lq[t % 3];  // L[t][s >= t] = 0
+                    part = fmaf(Lr[1], x[1], Lr[0] * x[0]) + fmaf(Lr[3], x[3], Lr[2] * x[2]);
+                }
+                part += dpp<0xB1>(part);  // quad: lanes p ^ 1
+                part += dpp<0x4E>(part);  // quad: lanes p ^ 2
+                const float xt = t < c ? 0.0f : (t == c ? 1.0f : -part);
+                if ((t >> 2) == p) x[t & 3] = xt;
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) sT[(o + 4 * p + m) * FP + o + c] = x[m];
+            // the upper-triangular blocks of M are zero
+            for (int bj = wave + 1; bj < 4; ++bj) st16(blk(sT, wave, bj), f4{0.0f, 0.0f, 0.0f, 0.0f}, 1.0f);
+        }
+        __syncthreads();
+        if (wave < 2) {  // 2. wave 0: M_10, wave 1: M_32 (scratch: L blocks (0, 1), (2, 3))
+            const int i = 2 * wave + 1, j = 2 * wave;
+            float* P = blk(sKK, j, i);
+            st16(P, mm16(blk(sKK, i, j), blk(sT, j, j), f4{0.0f, 0.0f, 0.0f, 0.0f}), 1.0f);
+            st16(blk(sT, i, j), mm16(blk(sT, i, i), P, f4{0.0f, 0.0f, 0.0f, 0.0f}), -1.0f);
+        }
+        __syncthreads();
+        {  // 3. wave w: block (i, j) = (2 + w / 2, w % 2); Q = C M_A in L blocks (j, i)
+            const int i = 2 + (wave >> 1), j = wave & 1;
+            f4 q = mm16(blk(sKK, i, 1), blk(sT, 1, j), f4{0.0f, 0.0f, 0.0f, 0.0f});
+            if (j == 0) q = mm16(blk(sKK, i, 0), blk(sT, 0, 0), q);
+            st16(blk(sKK, j, i), q, 1.0f);
+            __syncthreads();
+            f4 r = mm16(blk(sT, i, 2), blk(sKK, j, 2), f4{0.0f, 0.0f, 0.0f, 0.0f});
+            if (i == 3) r = mm16(blk(sT, 3, 3), blk(sKK, j, 3), r);
+            st16(blk(sT, i, j), r, -1.0f);
+        }
+        __syncthreads();
 
-    // ---- the record: T (f16 hi + lo) with 16-byte stores, the decays and G
-    uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
-    {
-        const int t = tid >> 2, j0 = 16 * (tid & 3);
-        h8 th[2], tl[2];
+        // ---- the record: T (f16 hi + lo) with 16-byte stores, the decays and G
+        uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+        {
+            const int t = tid >> 2, j0 = 16 * (tid & 3);
+            h8 th[2], tl[2];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float tv = sT[t * FP + j0 + e] * sBeta[j0 + e];  // T = M diag(beta)
-            th[e >> 3][e & 7] = f16_hi(tv), tl[e >> 3][e & 7] = f16_lo(tv);
-        }
-        const int o = (t * 64 + j0) * 2;
+            for (int e = 0; e < 16; ++e) {
+                const float tv = sT[t * FP + j0 + e] * sBeta[e2][j0 + e];  // T = M diag(beta)
+                th[e >> 3][e & 7] = f16_hi(tv), tl[e >> 3][e & 7] = f16_lo(tv);
+            }
+            const int o = (t * 64 + j0) * 2;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            *(h8*)(rec + kRecTHi + o + 16 * u) = th[u];
-            *(h8*)(rec + kRecTLo + o + 16 * u) = tl[u];
+            for (int u = 0; u < 2; ++u) {
+                *(h8*)(rec + kRecTHi + o + 16 * u) = th[u];
+                *(h8*)(rec + kRecTLo + o + 16 * u) = tl[u];
+            }
         }
-    }
-    if (tid < 64) {
-        const float GC = sEG[63];
-        const float G = sEG[tid];
-        float* dec = (float*)(rec + kRecDec);
-        dec[tid] = __expf(G);
-        dec[64 + tid] = __expf(GC - G);
-        dec[kRecG + tid] = G;
-        if (tid == 0) dec[128] = __expf(GC);
-        if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[tid]);
+        if (tid < 64) {
+            const float GC = sEG[e2][63];
+            const float G = sEG[e2][tid];
+            float* dec = (float*)(rec + kRecDec);
+            dec[tid] = __expf(G);
+            dec[64 + tid] = __expf(GC - G);
+            dec[kRecG + tid] = G;
+            if (tid == 0) dec[128] = __expf(GC);
+            if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[e2][tid]);
+        }
     }
 }
 
@@ -868,7 +890,7 @@ bool gdn_chunked_available() { return true; }
 
 template <bool BF16, bool VEC>
 static void chunked_kernels(const GdnChunkArgs& a, hipStream_t stream) {
-    launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(a.n_chunks, 32, (uint32_t)a.B), dim3(256), stream, a);
+    launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(a.n_chunks, 16, (uint32_t)a.B), dim3(256), stream, a);
     launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC>, dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), stream, a);
 }
 
