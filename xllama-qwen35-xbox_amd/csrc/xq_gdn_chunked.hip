@@ -584,6 +584,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         S[a2] = f4{v.x, v.y, v.z, v.w};
     }
     float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
+    // the first chunk's operands do not depend on 2^a (V is scaled at use): their
+    // loads go out with the state's and the maxima's
+    ScanOps<BF16, VEC> ops[2];
+    scan_load_all<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
 
     // ---- 2^a: the largest |S| entering the block and |v| of its columns over
     //      the prefill (the chunks' maxima from the prep) brought into [1, 2)
@@ -621,8 +625,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 #pragma unroll
     for (int a2 = 0; a2 < 2; ++a2) S[a2] *= vscale;
 
-    ScanOps<BF16, VEC> ops[2];
-    scan_load_all<BF16, VEC>(a, b, h, cb, 0, wave, lr, lg, ops[0]);
     // One chunk: C holds its operands (loaded a chunk ahead), the next chunk's
     // operands are loaded into Nx part by part.
     auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx, _Float16* kth, _Float16* ktl) {
