@@ -162,7 +162,7 @@ XQ_DEV void bf16_split3(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
     hi = __float_as_uint(x) & 0xffff0000u;
     const float r = x - __uint_as_float(hi);
     mid = __float_as_uint(r) & 0xffff0000u;
-    lo = __float_as_uint(r - __uint_as_float(mid)) & 0xffff0000u;  // at most 8 significant bits: exact
+    lo = __float_as_uint(r - __uint_as_float(mid));  // at most 8 significant bits: its low half is zero
 }
 
 // the high halves of a and b as one word (a low)
