@@ -244,8 +244,10 @@ int64_t xq_fa_split_rows(int64_t kv_len, int32_t split_mode);
 enum xq_gdn_mode {
     XQ_GDN_AUTO = 0,     /* step for T <= 64, chunked above */
     XQ_GDN_STEP = 1,     /* token-sequential recurrence */
-    XQ_GDN_CHUNKED = 2,  /* 64-token chunks in the UT form on the f16 matrix cores
-                            (f32 operands split into f16 hi + lo) */
+    XQ_GDN_CHUNKED = 2,  /* 64-token chunks in the UT form on the matrix cores (f32
+                            operands split into f16 hi + lo, or three bf16 terms
+                            against bf16 rows); q/k/v row strides of 2^25 bytes
+                            or more run the token-sequential kernel instead */
 };
 
 /* Pure predicate mirroring d3d12_gdn_supported (src/bridge/ggml_d3d12.cpp:77-109),

@@ -491,13 +491,21 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
                       ScanOps<BF16, VEC>& L) {
     const int kh = h % 16;
     n = min(n, a.n_chunks - 1);  // the prefetch past the last chunk re-reads it
+    const int row0 = n * kChunk;      // the chunk's first token
+    const int last = a.T - 1 - row0;  // the chunk's rows past T read row T - 1 instead
     const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+    // Row addresses are a wave-uniform base (sequence, head, chunk: scalar
+    // registers) plus a 32-bit per-lane offset (the host keeps the row strides
+    // below 2^25 bytes), so the loads take their base from SGPRs and the
+    // per-chunk address arithmetic stays off the vector ALU.
     if constexpr (PART == 0) {
-        const int tg = n * kChunk + 16 * wave + lr;  // A-operand row token
-        L.ok = tg < a.T;
-        const int tc = min(tg, a.T - 1);
-        const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tc * a.k_nb2 + (int64_t)kh * a.k_nb1;
-        const uint8_t* qr = a.q + (int64_t)b * a.q_nb3 + (int64_t)tc * a.q_nb2 + (int64_t)kh * a.q_nb1;
+        const int r = 16 * wave + lr;  // A-operand row of the chunk
+        L.ok = r <= last;
+        const uint32_t rc = (uint32_t)min(r, last);
+        const uint8_t* kb = a.k + (int64_t)b * a.k_nb3 + (int64_t)row0 * a.k_nb2 + (int64_t)kh * a.k_nb1;
+        const uint8_t* qb = a.q + (int64_t)b * a.q_nb3 + (int64_t)row0 * a.q_nb2 + (int64_t)kh * a.q_nb1;
+        const uint8_t* kr = kb + rc * (uint32_t)a.k_nb2;
+        const uint8_t* qr = qb + rc * (uint32_t)a.q_nb2;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             load_raw8<BF16, VEC>(kr, 32 * ks + 8 * lg, L.kw[ks]);
@@ -506,31 +514,31 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
     } else if constexpr (PART == 1) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const int o = ((16 * wave + lr) * 64 + 32 * ks + 8 * lg) * 2;
+            const uint32_t o = ((uint32_t)(16 * wave + lr) * 64u + 32u * ks + 8u * lg) * 2u;
             L.th[ks] = *(const h8*)(rec + kRecTHi + o);
             L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
         }
     } else if constexpr (PART == 2) {
-        const float* dec = (const float*)(rec + kRecDec);
-        L.eg = *(const float4*)(dec + 16 * wave + 4 * lg);
-        L.egc = *(const float4*)(dec + 64 + 16 * wave + 4 * lg);
-        L.eGC = dec[128];
-        L.gt = dec[kRecG + 16 * wave + lr];
+        const uint8_t* dec = rec + kRecDec;  // f32 values, byte offsets below
+        L.eg = *(const float4*)(dec + 4u * (uint32_t)(16 * wave + 4 * lg));
+        L.egc = *(const float4*)(dec + 4u * (uint32_t)(64 + 16 * wave + 4 * lg));
+        L.eGC = *(const float*)(dec + 4u * 128u);
+        L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + kRecG + 16 * jt + 4 * lg);
+        for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
     } else {
         L.vok = 0;
+        const uint8_t* vb = a.v + (int64_t)b * a.v_nb3 + (int64_t)row0 * a.v_nb2 + (int64_t)h * a.v_nb1;
+        const uint32_t co = (uint32_t)(kCols * cb + lr) * (BF16 ? 2u : 4u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int tg = n * kChunk + 16 * wave + 4 * lg + r;
-            L.vok |= (tg < a.T ? 1u : 0u) << r;
-            const int tc = min(tg, a.T - 1);
-            const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)tc * a.v_nb2 + (int64_t)h * a.v_nb1;
-            const int c = kCols * cb + lr;
+            const int rr = 16 * wave + 4 * lg + r;
+            L.vok |= (rr <= last ? 1u : 0u) << r;
+            const uint8_t* vr = vb + ((uint32_t)min(rr, last) * (uint32_t)a.v_nb2 + co);
             if constexpr (BF16)
-                L.vw[r] = ((const uint16_t*)vr)[c];
+                L.vw[r] = *(const uint16_t*)vr;
             else
-                L.vw[r] = ((const uint32_t*)vr)[c];
+                L.vw[r] = *(const uint32_t*)vr;
         }
     }
 }
@@ -900,6 +908,10 @@ hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {
     const int64_t T = L.v->ne[2], B = L.v->ne[3];
     const int64_t Tc = chunked_tokens(T, L.slots);
     if (Tc < 1) return gdn_step_launch(L, stream);  // every token needs its own snapshot
+    // the scan addresses a chunk's rows with 32-bit offsets from the chunk's first
+    // row: row strides of 2^25 bytes or more run token by token instead
+    for (const xq_tensor* t : {L.q, L.k, L.v})
+        if (t->nb[2] >= ((int64_t)1 << 25)) return gdn_step_launch(L, stream);
     if (L.workspace_bytes < gdn_chunked_workspace_bytes(T, B, L.slots, L.q->type == XQ_TYPE_BF16))
         return hipErrorInvalidValue;
     GdnChunkArgs a{};
