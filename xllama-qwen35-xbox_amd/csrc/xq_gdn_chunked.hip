@@ -81,7 +81,12 @@ constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
 constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, max|v|[8] at 136, G[64] at 192
 constexpr int kRecG = 192;                      // G offset in floats within the decays
 constexpr int kRecVmax = 136;                   // largest |v| of the chunk per 16-column block (floats)
-constexpr int kRecBytes = kRecDec + 1024;
+// P tiles (bf16 rows with 16-byte loads): tile (w, jt), jt <= w, of scan wave w
+// is 1 KB at kRecP + (w (w + 1) / 2 + jt) KB; lane l's 16 bytes at 16 l are its
+// four values of P[16w + l % 16][16jt + 4(l / 16) + i] as f16 hi, then f16 lo
+constexpr int kRecP = kRecDec + 1024;
+constexpr int kRecBytes = kRecP + 10 * 1024;
+XQ_DEV constexpr int p_tile(int w, int jt) { return kRecP + (w * (w + 1) / 2 + jt) * 1024; }
 
 struct GdnChunkArgs {
     const uint8_t* q;
@@ -187,12 +192,18 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     // 36 KB for bf16 rows (53 KB for f32 rows); after the products sK becomes M.
     __shared__ __attribute__((aligned(16))) _Float16 sK[64 * KP];    // K [t][i], then M f32 [64][FP]
     __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // L of one v-head
-    __shared__ float sG[2][64], sBeta[2][64], sEG[2][64];
+    __shared__ __attribute__((aligned(16))) float sG[2][64], sBeta[2][64], sEG[2][64];
     __shared__ uint32_t sVmax[2][kColBlocks];  // bits of the largest |v| per column block
     // f32 rows: the f16 remainders of K
     constexpr int NKL = BF16 ? 8 : 64 * KP;
     __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
     static_assert(64 * FP * 4 <= 64 * KP * 2, "LDS aliases");
+
+    // bf16 rows read as 16-byte words (RAW): K and Q stay bf16 in LDS and the
+    // products run on bf16 MFMA (exact operands); the P tiles are formed here
+    constexpr bool RAW = BF16 && VEC;
+    _Float16* sQ = (_Float16*)sKK;  // RAW: Q [t][i] until the products are done
+    static_assert(64 * FP * 4 >= 64 * KP * 2, "Q rows fit the L buffer");
 
     // v-heads kh and kh + 16 share k-head kh: K K^T is formed once for both
     const int n = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
@@ -207,8 +218,28 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         const int tg = t0 + t;
         const bool ok = tg < a.T;
         const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tg * a.k_nb2 + (int64_t)kh * a.k_nb1;
+        if constexpr (RAW) {
+            // rows past T: loads of row T - 1, zeroed (no conditional loads)
+            const int tc = min(tg, a.T - 1);
+            const uint8_t* kc = a.k + (int64_t)b * a.k_nb3 + (int64_t)tc * a.k_nb2 + (int64_t)kh * a.k_nb1;
+            const uint8_t* qc = a.q + (int64_t)b * a.q_nb3 + (int64_t)tc * a.q_nb2 + (int64_t)kh * a.q_nb1;
+            uint4 wk[4], wq[4];
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                wk[gi] = *(const uint4*)(kc + 2 * (32 * qt + 8 * gi));
+                wq[gi] = *(const uint4*)(qc + 2 * (32 * qt + 8 * gi));
+            }
+            const uint32_t m = ok ? ~0u : 0u;  // a mask, not a select of the arrays
+#pragma unroll
+            for (int gi = 0; gi < 4; ++gi) {
+                const uint4 x = wk[gi], y = wq[gi];
+                *(uint4*)(sK + t * KP + 32 * qt + 8 * gi) = make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+                *(uint4*)(sQ + t * KP + 32 * qt + 8 * gi) = make_uint4(y.x & m, y.y & m, y.z & m, y.w & m);
+            }
+        }
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
+            if constexpr (RAW) break;
             const int i0 = 32 * qt + 8 * gi;
             float xk[8];
             if (ok) {
@@ -269,6 +300,13 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         const int tile = wave * 4 + tt;
         const int mt = tile >> 2, nt = tile & 3;
         kk[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (RAW) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                kk[tt] = mfma_bf(*(const uint4*)(sK + (mt * 16 + lr) * KP + ks * 32 + 8 * lg),
+                                 *(const uint4*)(sK + (nt * 16 + lr) * KP + ks * 32 + 8 * lg), kk[tt]);
+            continue;
+        }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 bk = *(const h8*)(sK + (nt * 16 + lr) * KP + ks * 32 + 8 * lg);
@@ -282,7 +320,21 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             }
         }
     }
-    __syncthreads();  // K no longer read; G ready
+    // RAW: P^T = K Q^T for the scan wave w's tiles (token tile w of q, tiles
+    // jt <= w of k), the products the scan would form: lane (lr, lg) holds
+    // q_t . k_j for t = 16w + lr, j = 16jt + 4lg + i
+    f4 pq[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+        pq[jt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (RAW && jt <= wave) {  // wave-uniform
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                pq[jt] = mfma_bf(*(const uint4*)(sK + (16 * jt + lr) * KP + 32 * ks + 8 * lg),
+                                 *(const uint4*)(sQ + (16 * wave + lr) * KP + 32 * ks + 8 * lg), pq[jt]);
+        }
+    }
+    __syncthreads();  // K and Q no longer read; G ready
 
     // ---- per v-head: M = (I + L)^{-1} by blocks of 16 (T = M diag(beta) is
     //      formed at the record). With D_i = I + L_ii the unit lower-triangular
@@ -400,6 +452,25 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             dec[kRecG + tid] = G;
             if (tid == 0) dec[128] = __expf(GC);
             if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[e2][tid]);
+        }
+        if constexpr (RAW) {  // P[t][j] = (q_t . k_j) e^{G_t - G_j} (j <= t), f16 hi + lo
+            uint8_t* pr = rec + 16 * lane;
+            const float gt = sEG[e2][16 * wave + lr];
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                if (jt <= wave) {  // wave-uniform
+                    const f4 gj = *(const f4*)&sEG[e2][16 * jt + 4 * lg];
+                    h4 ph, pl;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool causal = jt < wave || 4 * lg + i <= lr;
+                        const float pv = causal ? pq[jt][i] * __expf(gt - gj[i]) : 0.0f;
+                        ph[i] = f16_hi(pv), pl[i] = f16_lo(pv);
+                    }
+                    const uint2 bh = __builtin_bit_cast(uint2, ph), bl = __builtin_bit_cast(uint2, pl);
+                    *(uint4*)(pr + p_tile(wave, jt)) = make_uint4(bh.x, bh.y, bl.x, bl.y);
+                }
+            }
         }
     }
 }
@@ -523,9 +594,11 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
         L.eg = *(const float4*)(dec + 4u * (uint32_t)(16 * wave + 4 * lg));
         L.egc = *(const float4*)(dec + 4u * (uint32_t)(64 + 16 * wave + 4 * lg));
         L.eGC = *(const float*)(dec + 4u * 128u);
-        L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
+        if constexpr (!(BF16 && VEC)) {  // bf16 rows with 16-byte loads take P from the record
+            L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
+            for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
+        }
     } else {
         L.vok = 0;
         const uint8_t* vb = a.v + (int64_t)b * a.v_nb3 + (int64_t)row0 * a.v_nb2 + (int64_t)h * a.v_nb1;
@@ -567,7 +640,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sWh[kCols * TP], sWl[kCols * TP];  // (e^{G_C - G} U)^T
     __shared__ __attribute__((aligned(16))) _Float16 sWm[RAW ? kCols * TP : 8];
     // K rows of the chunk [t][i] (f16 hi, and lo for f32 rows): the A operands of P^T = K Q^T
-    __shared__ __attribute__((aligned(16))) _Float16 sKh[64 * SP], sKl[BF16 ? 8 : 64 * SP];
+    __shared__ __attribute__((aligned(16))) _Float16 sKh[RAW ? 8 : 64 * SP], sKl[BF16 ? 8 : 64 * SP];
     // K^T [i][t] of the chunk, by chunk parity (read after the step's last
     // barrier, so the next chunk writes the other one): the A operands of the
     // state update
@@ -637,6 +710,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     // operands are loaded into Nx part by part.
     auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx, _Float16* kth, _Float16* ktl) {
         scan_load<0>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
+        // RAW: this chunk's P tiles from the record (formed by the prep), used
+        // by Y at the end of the step
+        uint4 pw[4];
+        if constexpr (RAW) {
+            const uint8_t* pr = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + nn) * kRecBytes + 16u * (uint32_t)lane;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                pw[jt] = make_uint4(0u, 0u, 0u, 0u);
+                if (jt <= wave) pw[jt] = *(const uint4*)(pr + p_tile(wave, jt));  // wave-uniform
+            }
+        }
 
         // ---- the wave's K rows -> LDS, as rows (every wave forms its P from
         //      all of them) and transposed (the state update's operands)
@@ -649,7 +733,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
                 // enter meets a zero T row or column, so they add nothing
                 rk[ks] = C.kw[ks][0];
                 rq[ks] = C.qw[ks][0];
-                *(uint4*)(sKh + (16 * wave + lr) * SP + 32 * ks + 8 * lg) = rk[ks];
                 const uint32_t u[4] = {rk[ks].x, rk[ks].y, rk[ks].z, rk[ks].w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
@@ -737,33 +820,35 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         // ---- P[t][j] = (q_t . k_j) e^{G_t - G_j} (j <= t) for t in the wave's
         //      tile, as P^T = K Q^T per token tile jt <= w: lane (lr, lg) gets
         //      t = 16w + lr, j = 16jt + 4lg + i, which is the A operand layout of
-        //      the 16x16x16 product Y += P U below
+        //      the 16x16x16 product Y += P U below. RAW: the prep formed them
+        //      (the same products), so they stay off the step's chain
         h4 ph[4], pl[4];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
             ph[jt] = h4{0, 0, 0, 0};
             pl[jt] = ph[jt];
-            if (jt > wave) continue;  // wave-uniform
-            f4 pt = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (RAW) {
+                ph[jt] = __builtin_bit_cast(h4, make_uint2(pw[jt].x, pw[jt].y));
+                pl[jt] = __builtin_bit_cast(h4, make_uint2(pw[jt].z, pw[jt].w));
+            } else {
+                if (jt > wave) continue;  // wave-uniform
+                f4 pt = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int ko = (16 * jt + lr) * SP + 32 * ks + 8 * lg;
-                if constexpr (RAW) {
-                    pt = mfma_bf(*(const uint4*)(sKh + ko), rq[ks], pt);
-                    continue;
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int ko = (16 * jt + lr) * SP + 32 * ks + 8 * lg;
+                    const h8 kj = *(const h8*)(sKh + ko);
+                    pt = mfma32(kj, aq[ks], pt);
+                    if constexpr (!BF16) {
+                        pt = mfma32(kj, decode8_lo(C.qw[ks], C.ok), pt);
+                        pt = mfma32(*(const h8*)(sKl + ko), aq[ks], pt);
+                    }
                 }
-                const h8 kj = *(const h8*)(sKh + ko);
-                pt = mfma32(kj, aq[ks], pt);
-                if constexpr (!BF16) {
-                    pt = mfma32(kj, decode8_lo(C.qw[ks], C.ok), pt);
-                    pt = mfma32(*(const h8*)(sKl + ko), aq[ks], pt);
-                }
-            }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool causal = jt < wave || 4 * lg + i <= lr;
-                const float pv = causal ? pt[i] * __expf(C.gt - C.gj[jt][i]) : 0.0f;
-                ph[jt][i] = f16_hi(pv), pl[jt][i] = f16_lo(pv);
+                for (int i = 0; i < 4; ++i) {
+                    const bool causal = jt < wave || 4 * lg + i <= lr;
+                    const float pv = causal ? pt[i] * __expf(C.gt - C.gj[jt][i]) : 0.0f;
+                    ph[jt][i] = f16_hi(pv), pl[jt][i] = f16_lo(pv);
+                }
             }
         }
         __syncthreads();
