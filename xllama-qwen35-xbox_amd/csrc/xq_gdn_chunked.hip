@@ -21,24 +21,29 @@
 //                   f16 MFMA once (f32 accumulation) and, per v-head, the unit
 //                   lower-triangular inverse for T in f32 (by 16 x 16 blocks,
 //                   the products on f32 MFMA); stores T as f16 hi + lo
-//                   planes, the decay vectors, the cumulative log-decays G and
-//                   the chunk's largest |v| per 16-column block (17 KB per
-//                   chunk) in the workspace. f32 k rows enter as f16 hi + lo
+//                   planes, the decay vectors, the cumulative log-decays G,
+//                   the chunk's largest |v| per 16-column block and, for bf16
+//                   rows read as 16-byte words, the P tiles (f16 hi + lo; 27 KB
+//                   per chunk) in the workspace. f32 k rows enter as f16 hi + lo
 //                   (the products take hi*hi + hi*lo + lo*hi); bf16 rows enter
 //                   as f16 (their 8 significant bits fit; a bf16 value below
 //                   2^-14 keeps an absolute precision of 2^-25 there, not its
-//                   relative one).
+//                   relative one), or as bf16 on bf16 MFMA when read as
+//                   16-byte words (exact).
 //   gdn_chunk_scan  one workgroup per (sequence, v-head, 16 value columns) runs
 //                   the chunks in order with its 128 x 16 state block in
 //                   registers (f32). Every MFMA operand that does not depend on
 //                   the state (K and Q rows straight from the inputs, as f16,
 //                   or f16 hi + lo for f32 rows; T rows from the workspace; V,
 //                   the decays and G) is loaded into registers a chunk ahead,
-//                   in four parts spread over the chunk's phases. P and K^T are
-//                   formed in the scan from the K and Q rows it already holds
-//                   (the waves share their K rows through LDS, as rows and
-//                   transposed), which keeps 32 KB per chunk out of every
-//                   workgroup's operand fetch, the scan's limit. LDS otherwise
+//                   in four parts spread over the chunk's phases. K^T is formed
+//                   in the scan from the K rows it already holds (the waves
+//                   share them through LDS, transposed), which keeps 16 KB per
+//                   chunk out of every workgroup's operand fetch. P is formed
+//                   by the prep for bf16 rows read as 16-byte words (10 KB per
+//                   chunk, off the scan's chain; its products and decays are
+//                   the scan's own), and by the scan from its K and Q rows
+//                   (shared through LDS) otherwise. LDS otherwise
 //                   carries the state-dependent exchanges (S^T, X^T, U^T). The products run
 //                   on f16 MFMA with f32 operands split into f16 hi + lo (about
 //                   22 significant bits), so the result stays within
@@ -480,15 +485,18 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
 // Operands of one chunk for one wave of a scan workgroup, loaded a chunk ahead:
 // A operands (row 16w + lr of the wave's token tile, k = 32 ks + 8 lg .. +7) of
 // K and Q (raw input words, decoded when used) and of T (hi, lo); the raw V
-// values and e^G, e^{G_C - G}
-// of the lane's four tokens 16w + 4lg + r (column 16cb + lr), e^{G_C}, and the
-// G values P needs (token 16w + lr, tokens 16jt + 4lg + i). Every load is unconditional (token and chunk indices are clamped
-// into range and out-of-range tokens masked at use), so the compiler's waits
-// for a chunk's operands never include the next chunk's loads.
+// values and e^G, e^{G_C - G} of the lane's four tokens 16w + 4lg + r (column
+// 16cb + lr), e^{G_C}; for bf16 rows read as 16-byte words the wave's P tiles
+// from the record, otherwise the G values the scan's P needs (token 16w + lr,
+// tokens 16jt + 4lg + i). The loads are unconditional but for the P tiles (one
+// per tile jt <= w, a count fixed per wave): token and chunk indices are
+// clamped into range and out-of-range tokens masked at use, so the compiler's
+// waits for a chunk's operands never include the next chunk's loads.
 template <bool BF16, bool VEC>
 struct ScanOps {
     static constexpr int KW = VEC ? (BF16 ? 1 : 2) : 4;  // 16-byte words per 8 elements (VEC), else raw dwords
     uint4 kw[4][KW], qw[4][KW];
+    uint4 pw[4];  // bf16 rows with 16-byte loads: the wave's P tiles (w, jt <= w) from the record
     h8 th[2], tl[2];
     // raw V words, in the input's width: a 16-bit load widened at use (widened
     // here, the compiler copies the value at the loop edge and waits for it)
@@ -594,7 +602,11 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
         L.eg = *(const float4*)(dec + 4u * (uint32_t)(16 * wave + 4 * lg));
         L.egc = *(const float4*)(dec + 4u * (uint32_t)(64 + 16 * wave + 4 * lg));
         L.eGC = *(const float*)(dec + 4u * 128u);
-        if constexpr (!(BF16 && VEC)) {  // bf16 rows with 16-byte loads take P from the record
+        if constexpr (BF16 && VEC) {  // bf16 rows with 16-byte loads: the P tiles from the record
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt)
+                if (jt <= wave) L.pw[jt] = *(const uint4*)(rec + 16u * (uint32_t)(lr + 16 * lg) + p_tile(wave, jt));  // wave-uniform
+        } else {
             L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
@@ -710,18 +722,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     // operands are loaded into Nx part by part.
     auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx, _Float16* kth, _Float16* ktl) {
         scan_load<0>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
-        // RAW: this chunk's P tiles from the record (formed by the prep), used
-        // by Y at the end of the step
-        uint4 pw[4];
-        if constexpr (RAW) {
-            const uint8_t* pr = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + nn) * kRecBytes + 16u * (uint32_t)lane;
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                pw[jt] = make_uint4(0u, 0u, 0u, 0u);
-                if (jt <= wave) pw[jt] = *(const uint4*)(pr + p_tile(wave, jt));  // wave-uniform
-            }
-        }
-
         // ---- the wave's K rows -> LDS, as rows (every wave forms its P from
         //      all of them) and transposed (the state update's operands)
         h8 ak[4], aq[4];
@@ -827,9 +827,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         for (int jt = 0; jt < 4; ++jt) {
             ph[jt] = h4{0, 0, 0, 0};
             pl[jt] = ph[jt];
-            if constexpr (RAW) {
-                ph[jt] = __builtin_bit_cast(h4, make_uint2(pw[jt].x, pw[jt].y));
-                pl[jt] = __builtin_bit_cast(h4, make_uint2(pw[jt].z, pw[jt].w));
+            if constexpr (RAW) {  // the prep's tiles, loaded a chunk ahead
+                if (jt > wave) continue;  // wave-uniform
+                ph[jt] = __builtin_bit_cast(h4, make_uint2(C.pw[jt].x, C.pw[jt].y));
+                pl[jt] = __builtin_bit_cast(h4, make_uint2(C.pw[jt].z, C.pw[jt].w));
             } else {
                 if (jt > wave) continue;  // wave-uniform
                 f4 pt = f4{0.0f, 0.0f, 0.0f, 0.0f};
