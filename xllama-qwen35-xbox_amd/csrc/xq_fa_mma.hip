@@ -26,24 +26,25 @@
 //           both exact, so every product, and so every score, is ggml's.
 //           F16 / E5M2 K: v_mfma_f32_16x16x32_f16 on the exact f16 K with Q
 //           split into f16 hi + lo parts (the NATIVE policy uses hi alone).
-//   values  O^T = V^T W^T over 32 products per MFMA, A = 16 head dims,
-//           B = the weights of 16 pairs. The score tile's output registers
-//           (lane = pair, four consecutive rows) hold exactly the rows a lane
-//           gives the B operand, so the softmax weights never leave registers
-//           and every per-pair quantity (maximum, sum, rescale factor) is
-//           lane-local. Each weight enters as a high and a low part (products
-//           8lg..8lg+3 of a lane group: its four rows' high parts, 8lg+4..
-//           8lg+7: their low parts; the V operand repeats the four rows), so
-//           the product carries ~22 (f16) or ~16 (bf16) significant bits of
-//           every weight:
-//           q8_0 / q4_0 V: v_mfma_f32_16x16x32_bf16 on the exact integer
-//           values (bf16 holds every int8) against w * d_v formed in f32 and
-//           split into bf16 high (truncated) + low (rounded) parts; bf16 has
-//           f32's exponent range, so the value path is exact in range for any
-//           block scale (an f16 product w * d_v falls into subnormals, and
-//           then to zero, as V's magnitude shrinks);
+//   values  O^T = V^T W^T, A = 16 head dims x the slice's rows, B = the
+//           weights of 16 pairs. The score tile's output registers (lane =
+//           pair, four consecutive rows) hold exactly the rows a lane gives
+//           the B operand, so the softmax weights never leave registers and
+//           every per-pair quantity (maximum, sum, rescale factor) is
+//           lane-local.
+//           q8_0 / q4_0 V: v_mfma_f32_16x16x16_f16 on the exact integer values
+//           as f16 against w * 2^S_p * d_v, each product formed in f32 by one
+//           v_fma_mix and rounded once to f16. 2^S_p, a power of two per pair
+//           sized from the block scales the pair has seen, keeps every product
+//           in f16's normal range whatever V's scale (a product w * d_v would
+//           fall into subnormals, and then to zero, as V's magnitude shrinks);
+//           it enters the weights' exponent argument and leaves at the merge,
+//           both exactly.
 //           F16 / E5M2 V: v_mfma_f32_16x16x32_f16 on the exact f16 V against
-//           the weight in f16 high + low parts (the weights lie in (0, 16]).
+//           the weight as f16 high + low parts (products 8lg..8lg+3 of a lane
+//           group: its four rows' high parts, 8lg+4..8lg+7: their low parts;
+//           the V operand repeats the four rows), about 22 significant bits of
+//           every weight (the weights lie in (0, 16]).
 // Online softmax in base 2 (scores pre-multiplied by log2 e) with a lazy
 // maximum: the running maximum moves only when a slice exceeds it by more
 // than 8, so accumulator rescales are rare; weights are taken relative to the
@@ -52,8 +53,9 @@
 // Rows a pair does not see (mask -inf, past its causal limit or the split)
 // never touch its state, as ggml's loop skips them: a slice that holds such a
 // row or a non-finite score runs "careful" — the scores of unseen rows become
-// -inf whatever K holds, quantized V weights of unseen rows are zeroed before
-// the scale multiplies them, and non-finite F16/E5M2 V elements are replaced
+// -inf whatever K holds, the weight x scale products of quantized V's unseen
+// rows are masked to +0 whatever their scale holds, and non-finite F16/E5M2 V
+// elements are replaced
 // by 0 in the shared V operand while every pair that sees such a row gets a
 // NaN state. Range calls (positions) additionally turn a row whose output or
 // normaliser is not finite into NaN in full (the split reducer's poisoning).
