@@ -198,9 +198,8 @@ def test_gdn_predicate():
 
 def test_gdn_workspace_query():
     """AUTO runs prefills longer than one chunk on the chunked kernels: one
-    workspace record of 17408 bytes per (sequence,
-    v-head, 64-token chunk) of the first T - (slots - 1) tokens; the step
-    kernel needs none."""
+    workspace record of 27648 bytes per (sequence, v-head, 64-token chunk) of
+    the first T - (slots - 1) tokens; the step kernel needs none."""
     l = lib()
     n = ctypes.c_size_t(0)
 
@@ -210,7 +209,7 @@ def test_gdn_workspace_query():
         assert l.xq_gated_delta_net_workspace(ctypes.byref(q), ctypes.byref(v), slots, mode, ctypes.byref(n)) == 0
         return n.value
 
-    rec = 2 * 64 * 64 * 2 + 1024  # T (f16 hi, lo), decays and G
+    rec = 2 * 64 * 64 * 2 + 1024 + 10 * 1024  # T (f16 hi, lo), decays and G, the P tiles
     assert need(4096, 1, 1, xqattn.GDN_AUTO, wl.F32) == 32 * 64 * rec  # the same record for f32 rows
     assert need(200, 2, 3, xqattn.GDN_CHUNKED) == 2 * 32 * 4 * rec  # 198 tokens -> 4 chunks
     assert need(4096, 1, 1, xqattn.GDN_AUTO) == 32 * 64 * rec
