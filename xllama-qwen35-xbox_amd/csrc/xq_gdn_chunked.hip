@@ -561,6 +561,12 @@ XQ_DEV h8 decode8(const uint4 (&w)[KW], bool ok) {
     return r;
 }
 
+// A buffer resource over one workspace record (raw: byte offsets, no stride;
+// the record is far below the 2^31-byte range it allows).
+XQ_DEV __amdgpu_buffer_rsrc_t rec_rsrc(const uint8_t* rec) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)rec, (short)0, 0x7fffffff, 0x00020000);
+}
+
 // The operands of chunk n in four parts, each issued in its own phase of the
 // previous chunk's step (between its barriers), in the order the step uses
 // them: a burst of all of them at the start of a step stalls the wave while
@@ -583,33 +589,69 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
         const uint32_t rc = (uint32_t)min(r, last);
         const uint8_t* kb = a.k + (int64_t)b * a.k_nb3 + (int64_t)row0 * a.k_nb2 + (int64_t)kh * a.k_nb1;
         const uint8_t* qb = a.q + (int64_t)b * a.q_nb3 + (int64_t)row0 * a.q_nb2 + (int64_t)kh * a.q_nb1;
-        const uint8_t* kr = kb + rc * (uint32_t)a.k_nb2;
-        const uint8_t* qr = qb + rc * (uint32_t)a.q_nb2;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            load_raw8<BF16, VEC>(kr, 32 * ks + 8 * lg, L.kw[ks]);
-            load_raw8<BF16, VEC>(qr, 32 * ks + 8 * lg, L.qw[ks]);
+            if constexpr (VEC) {  // the lane's part of the offset in one 32-bit word
+                const uint32_t eo = (BF16 ? 2u : 4u) * (8u * (uint32_t)lg);
+                const uint32_t ko = rc * (uint32_t)a.k_nb2 + eo, qo = rc * (uint32_t)a.q_nb2 + eo;
+#pragma unroll
+                for (int u = 0; u < ScanOps<BF16, VEC>::KW; ++u) {
+                    L.kw[ks][u] = *(const uint4*)(kb + (BF16 ? 64 : 128) * ks + 16 * u + ko);
+                    L.qw[ks][u] = *(const uint4*)(qb + (BF16 ? 64 : 128) * ks + 16 * u + qo);
+                }
+            } else {
+                load_raw8<BF16, VEC>(kb + rc * (uint32_t)a.k_nb2, 32 * ks + 8 * lg, L.kw[ks]);
+                load_raw8<BF16, VEC>(qb + rc * (uint32_t)a.q_nb2, 32 * ks + 8 * lg, L.qw[ks]);
+            }
         }
     } else if constexpr (PART == 1) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const uint32_t o = ((uint32_t)(16 * wave + lr) * 64u + 32u * ks + 8u * lg) * 2u;
-            L.th[ks] = *(const h8*)(rec + kRecTHi + o);
-            L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
+            if constexpr (BF16 && VEC) {
+                const __amdgpu_buffer_rsrc_t r = rec_rsrc(rec);
+                L.th[ks] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, o, kRecTHi, 0));
+                L.tl[ks] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(r, o, kRecTLo, 0));
+            } else {
+                L.th[ks] = *(const h8*)(rec + kRecTHi + o);
+                L.tl[ks] = *(const h8*)(rec + kRecTLo + o);
+            }
         }
+    } else if constexpr (PART == 2 && BF16 && VEC) {
+        // the record through a buffer resource: uniform parts of the offsets in
+        // SGPRs, the lane's part in one VGPR, no per-load address arithmetic
+        const __amdgpu_buffer_rsrc_t r = rec_rsrc(rec);
+        const uint32_t eo = 4u * (uint32_t)(16 * wave + 4 * lg);
+        L.eg = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, eo, kRecDec, 0));
+        L.egc = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, eo, kRecDec + 256, 0));
+        L.eGC = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, 0u, kRecDec + 512, 0));
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+            if (jt <= wave)  // wave-uniform
+                L.pw[jt] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * (uint32_t)(lr + 16 * lg), p_tile(wave, jt), 0));
     } else if constexpr (PART == 2) {
         const uint8_t* dec = rec + kRecDec;  // f32 values, byte offsets below
         L.eg = *(const float4*)(dec + 4u * (uint32_t)(16 * wave + 4 * lg));
         L.egc = *(const float4*)(dec + 4u * (uint32_t)(64 + 16 * wave + 4 * lg));
         L.eGC = *(const float*)(dec + 4u * 128u);
-        if constexpr (BF16 && VEC) {  // bf16 rows with 16-byte loads: the P tiles from the record
+        L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt)
-                if (jt <= wave) L.pw[jt] = *(const uint4*)(rec + 16u * (uint32_t)(lr + 16 * lg) + p_tile(wave, jt));  // wave-uniform
-        } else {
-            L.gt = *(const float*)(dec + 4u * (uint32_t)(kRecG + 16 * wave + lr));
+        for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
+    } else if constexpr (BF16 && VEC) {
+        // the chunk's V rows through a buffer resource whose range ends after
+        // row `last` (row offsets below 2^25 bytes): a row past it reads 0
+        // without touching memory (and is masked at use), so the lane offsets
+        // need no clamp and stay the same for every chunk
+        L.vok = 0;
+        const uint8_t* vb = a.v + (int64_t)b * a.v_nb3 + (int64_t)row0 * a.v_nb2 + (int64_t)h * a.v_nb1;
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, (int)((uint32_t)min(last, kChunk - 1) * (uint32_t)a.v_nb2 + 256u), 0x00020000);
+        const uint32_t co = (uint32_t)(kCols * cb + lr) * 2u;
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) L.gj[jt] = *(const f4*)(dec + 4u * (uint32_t)(kRecG + 16 * jt + 4 * lg));
+        for (int q = 0; q < 4; ++q) {
+            const int rr = 16 * wave + 4 * lg + q;
+            L.vok |= (rr <= last ? 1u : 0u) << q;
+            L.vw[q] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)rr * (uint32_t)a.v_nb2 + co, 0, 0);
         }
     } else {
         L.vok = 0;
@@ -904,10 +946,25 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
             y2 = mfma16(pl[jt], bh, y2);
         }
         y += y2;
+        if constexpr (RAW) {
+            // through a buffer resource over the chunk's output rows: the
+            // (head, column block) part of the offset in an SGPR, the lane's
+            // token and column in one VGPR
+            const __amdgpu_buffer_rsrc_t r =
+                __builtin_amdgcn_make_buffer_rsrc((void*)(out + (int64_t)nn * kChunk * 4096), (short)0, 0x7fffffff, 0x00020000);
+            const uint32_t so = 4u * (uint32_t)(h * 128 + kCols * cb);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = nn * kChunk + 16 * wave + 4 * lg + r;
-            if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[r] * yscale;
+            for (int q = 0; q < 4; ++q) {
+                const int tl = 16 * wave + 4 * lg + q;  // token within the chunk
+                if (nn * kChunk + tl < a.T)
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[q] * yscale), r, (uint32_t)tl * 16384u + 4u * (uint32_t)lr, so, 0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int t = nn * kChunk + 16 * wave + 4 * lg + q;
+                if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[q] * yscale;
+            }
         }
 
         // ---- S = e^{G_C} S + K^T (e^{G_C - G} U) for this wave's key-dim tiles
