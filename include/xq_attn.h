@@ -126,9 +126,12 @@ enum xq_fa_split_mode {
 
 /* Which pass-1 kernel computes the scores and the value product.
  *  XQ_FA_ENGINE_AUTO: the matrix-core kernel where it exists (q8_0/q4_0 K with
- *    integer scores, F16/E5M2 K), else the VALU kernel.
+ *    integer scores, F16/E5M2 K), else the VALU kernel. Its quantized-V value
+ *    products (weight x block scale) are rounded once to f16 (2^-11 relative
+ *    each); F16/E5M2 V weights enter as f16 hi + lo.
  *  XQ_FA_ENGINE_MFMA: the matrix-core kernel (UNSUPPORTED where it does not exist).
- *  XQ_FA_ENGINE_VALU: the vector-ALU kernel (dot4 integer scores, f32 FMA values). */
+ *  XQ_FA_ENGINE_VALU: the vector-ALU kernel (dot4 integer scores, f32 FMA values:
+ *    ggml's f32 value products, slower). */
 enum xq_fa_engine {
     XQ_FA_ENGINE_AUTO = 0,
     XQ_FA_ENGINE_MFMA = 1,
