@@ -764,8 +764,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     // operands are loaded into Nx part by part.
     auto chunk = [&](const int nn, ScanOps<BF16, VEC>& C, ScanOps<BF16, VEC>& Nx, _Float16* kth, _Float16* ktl) {
         scan_load<0>(a, b, h, cb, nn + 1, wave, lr, lg, Nx);
-        // ---- the wave's K rows -> LDS, as rows (every wave forms its P from
-        //      all of them) and transposed (the state update's operands)
+
+        // ---- the wave's K rows -> LDS transposed (the state update's
+        //      operands) and, when the scan forms P, as rows (every wave forms
+        //      its P from all of them)
         h8 ak[4], aq[4];
         uint4 rk[4], rq[4];  // RAW: the rows as loaded
 #pragma unroll
