@@ -602,6 +602,28 @@ def main():
         if args.only == "prefill":
             out.update({"value": round(p_alg / (p_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(p_ms, 5), "config": {"workload": pcfg.name}})
+        # the same prefill for 8 sequences at once (one input set of 1.1 GB, beyond
+        # the Infinity Cache): throughput when the scan has more than one
+        # workgroup per CU to run
+        bcfg = wl.GDN_C4_B8
+        bsets = make_gdn_sets(torch, xq, wl, bcfg, 1, seed=5)
+        b_ws = torch.empty(xq.gated_delta_net_workspace(bsets[0][0], bsets[0][2], bcfg.slots, xq.GDN_CHUNKED) + 256,
+                           dtype=torch.uint8, device="cuda")
+
+        def prefill8_call(i):
+            xq.gated_delta_net(*bsets[i], bcfg.slots, mode=xq.GDN_CHUNKED, workspace=b_ws)
+
+        b_steps = max(args.steps // 5, 5)
+        b_stats = {}
+        b_ms, _ = graph_time(torch, prefill8_call, 1, b_steps, max(args.warmup // 2, 2), b_stats)
+        bkt = kernel_times(torch, xq, prefill8_call, 1, b_steps)
+        b_alg = bcfg.algorithmic_bytes()
+        log(f"GDN prefill x8: {b_ms * 1000:.2f} us/call; kernels {bkt}")
+        out["gdn_prefill"]["b8"] = {"workload": bcfg.name, "us_per_call": round(b_ms * 1000, 3),
+                                    "algorithmic_bytes": b_alg, "call_GB/s": round(b_alg / (b_ms * 1e-3) / 1e9, 1),
+                                    "tokens_per_s": round(bcfg.T * bcfg.B / (b_ms * 1e-3), 1),
+                                    "call_us_dist": b_stats, "kernels": bkt}
+        del bsets, b_ws
 
     # ---------------- CPU baselines (ggml-CPU semantics restated, this host's cores)
     if not args.no_cpu:

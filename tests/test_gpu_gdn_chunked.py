@@ -42,6 +42,16 @@ def test_gdn_chunked_prefill_4096_bf16(torch_gpu):
     print(f"C4: max|gpu-oracle|={err:.2e} max|gpu-f64|={err64:.2e}")
 
 
+def test_gdn_chunked_prefill_8_sequences(torch_gpu):
+    """8 bf16 sequences of 1089 tokens at once (2048 scan workgroups, several per
+    CU, and a one-token last chunk) against the restated recurrence."""
+    case_note("gated_delta_net chunked T=1089 B=8 bf16")
+    case = make_gdn_case(1089, 1, B=8, dist="north_star", bf16=True, seed=78)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    err = _check(case, got, case.oracle(), "chunked x8 vs restated recurrence")
+    print(f"T=1089 B=8: max|gpu-oracle|={err:.2e}")
+
+
 @pytest.mark.parametrize("bf16", [True, False])
 @pytest.mark.parametrize("T,slots,B", [(65, 1, 1), (100, 1, 2), (128, 1, 1), (130, 3, 1),
                                        (200, 17, 1), (257, 5, 2), (64, 1, 1), (7, 2, 1)])

@@ -209,6 +209,7 @@ class GdnConfig:
 
 GDN_C3 = GdnConfig("gdn_step_hk16_hv32_d128_b8", T=1, B=8, slots=1)
 GDN_C4 = GdnConfig("gdn_prefill_T4096_c64_bf16", T=4096, B=1, slots=1, bf16=True)
+GDN_C4_B8 = GdnConfig("gdn_prefill_T4096_c64_bf16_b8", T=4096, B=8, slots=1, bf16=True)  # 8 sequences at once
 
 
 def fa_causal_mask(cfg: FaConfig, n_q_rows: int | None = None) -> np.ndarray:
