@@ -28,8 +28,9 @@ XQ_DEV float e5m2_to_f32(uint32_t b) { return f16_bits_to_f32((b & 0xffu) << 8);
 // host conversion.
 XQ_DEV uint32_t f32_to_f16_bits(float x) {
     const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7e00u;
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+    const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+    // a select, not a branch: callers convert whole rows with their loads in flight
+    return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) & 0x8000u) | 0x7e00u : h;
 }
 
 // Sign-extended int8 lane k (0..3) of a dword.

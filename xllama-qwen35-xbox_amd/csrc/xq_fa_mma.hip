@@ -504,20 +504,30 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             k_unit(t0, 0);
             v_unit(t0, 0);
         }
+        // The pair's f32 Q elements, every load issued before any is used (a
+        // padding pair reads pair 0's row, always valid, and is zeroed at use):
+        // one round trip in all, overlapping stage 0's
+        float xq[MT][NB][8];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const int p = 16 * m + lr;
-            const float* src = nullptr;  // f32 Q row of the pair
-            if (p < npa) {
-                const int qq = p / a.G, h = g_kv * a.G + p % a.G;
-                src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
-            }
+            const int pp = p < npa ? p : 0;
+            const int qq = pp / a.G, h = g_kv * a.G + pp % a.G;
+            const float* src = (const float*)(a.q + (int64_t)b * a.q_nb3 + (int64_t)(iq0 + qq) * a.q_nb1 + (int64_t)h * a.q_nb2);
+#pragma unroll
+            for (int c = 0; c < NB; ++c)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xq[m][c][j] = src[32 * c + 8 * lg + j];
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const bool ok = 16 * m + lr < npa;
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
                 // Q = f16 hi + f16 lo (lo = 0 for the NATIVE policy); NaN as ggml's f16 conversion
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float xv = src ? src[32 * c + 8 * lg + j] : 0.0f;
+                    const float xv = ok ? xq[m][c][j] : 0.0f;
                     const uint32_t hb = f32_to_f16_bits(xv);
                     qh[m][c][j] = __builtin_bit_cast(_Float16, (uint16_t)hb);
                     ql[m][c][j] = HI_ONLY ? (_Float16)0.0f
