@@ -757,7 +757,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     if (lane == 0) sProg[wave] = 0;
     auto balance = [&]() {
         if constexpr (NW == 8) {
-            const int other = *(volatile int*)&sProg[wave ^ 4];
+            const int other = __hip_atomic_load(&sProg[wave ^ 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (done < other || (done == other && wave >= 4))
                 __builtin_amdgcn_s_setprio(1);
             else
@@ -1005,14 +1005,14 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             v_unit(t + 2 * step, S);
         }
         ++done;
-        if (NW == 8 && lane == 0) *(volatile int*)&sProg[wave] = done;
+        if (NW == 8 && lane == 0) __hip_atomic_store(&sProg[wave], done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
     for (; t0 < r_end; t0 += 2 * step) {
         slice(t0, std::integral_constant<int, 0>{});
         if (t0 + step < r_end) slice(t0 + step, std::integral_constant<int, 1>{});
     }
     __builtin_amdgcn_s_setprio(0);
-    if (NW == 8 && lane == 0) *(volatile int*)&sProg[wave] = 1 << 30;  // done: never behind
+    if (NW == 8 && lane == 0) __hip_atomic_store(&sProg[wave], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);  // done: never behind
 
     // ---- merge the wave states per 16-pair group through LDS (fixed wave order)
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
