@@ -33,7 +33,8 @@
 //           every per-pair quantity (maximum, sum, rescale factor) is
 //           lane-local.
 //           q8_0 / q4_0 V: v_mfma_f32_16x16x16_f16 on the exact integer values
-//           as f16 against w * 2^S_p * d_v, each product formed in f32 by one
+//           as f16 (q4_0's high nibbles as 16x theirs, undone exactly at the
+//           merge) against w * 2^S_p * d_v, each product formed in f32 by one
 //           v_fma_mix and rounded once to f16. 2^S_p, a power of two per pair
 //           sized from the block scales the pair has seen, keeps every product
 //           in f16's normal range whatever V's scale (a product w * d_v would
@@ -66,6 +67,7 @@
 namespace xq {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -562,6 +564,11 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     const float cap2 = a.softcap * kLog2e;
 
     f4 acc[MT][2 * NB];
+    // the f16 pair (1024, 1024) in a VGPR, opaque to constant folding: each
+    // q4_0 value operand half then takes one v_and_or (a VOP3 cannot hold it
+    // as a literal)
+    uint32_t k6400 = 0;
+    if constexpr (KT == XQ_TYPE_Q4_0) asm("v_mov_b32 %0, 0x64006400" : "=v"(k6400));
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -648,17 +655,27 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         constexpr bool careful = decltype(careful_tag)::value;  // a separate copy: no mask selects when false
         const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
         uint32_t X[4];
+        if constexpr (KT == XQ_TYPE_Q4_0) {
+            // byte lr of rows (0,1) and (2,3) as the halves of X[0], X[1]
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint8_t* vr = Vs + (4 * lg + e) * REC;
-            if constexpr (KT == XQ_TYPE_Q8_0)
-                X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
-            else if constexpr (KT == XQ_TYPE_Q4_0)
-                X[e] = *(const uint8_t*)(vr + 18 * c + 2 + lr);
-            else if constexpr (KT == XQ_TYPE_F16)
-                X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
-            else
-                X[e] = lds_u16(vr + 32 * c + 2 * lr);
+            for (int e = 0; e < 2; ++e) {
+                const uint8_t* vr = Vs + (4 * lg + 2 * e) * REC + 18 * c + 2 + lr;
+                u16x2 p;
+                p.x = vr[0];
+                p.y = vr[REC];
+                X[e] = __builtin_bit_cast(uint32_t, p);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint8_t* vr = Vs + (4 * lg + e) * REC;
+                if constexpr (KT == XQ_TYPE_Q8_0)
+                    X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
+                else if constexpr (KT == XQ_TYPE_F16)
+                    X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
+                else
+                    X[e] = lds_u16(vr + 32 * c + 2 * lr);
+            }
         }
         if constexpr (QUANT) {
             // B: w * 2^S * d_v rounded once to f16 (rows (0,1), (2,3)); the
@@ -685,15 +702,18 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             uint32_t A0[2], A1[2];
             if constexpr (KT == XQ_TYPE_Q8_0) {
                 q8_vt_f16(X[0], X[1], X[2], X[3], A0, A1);
-            } else {  // q4_0: low nibble (dim lr of the block), high nibble (dim 16 + lr), 1024 + n - 1032
+            } else {
+                // q4_0: the low nibble n (dim lr of the block) as 1024 + n - 1032 =
+                // n - 8, the high nibble (dim 16 + lr) unshifted as 1024 + 16n - 1152
+                // = 16(n - 8); both exact. Tile 1's accumulators hold 16x their
+                // values (every rounding scales with them) until the merge.
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
-                    const h2 bias = h2{(_Float16)-1032.0f, (_Float16)-1032.0f};
-                    const uint32_t w = X[2 * e] | (X[2 * e + 1] << 16);
-                    const uint32_t lo = (w & 0x000f000fu) | 0x64006400u;
-                    const uint32_t hi = ((w >> 4) & 0x000f000fu) | 0x64006400u;
-                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + bias);
-                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + bias);
+                    const uint32_t w = X[e];
+                    const uint32_t lo = (w & 0x000f000fu) | k6400;
+                    const uint32_t hi = (w & 0x00f000f0u) | k6400;
+                    A0[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, lo) + h2{(_Float16)-1032.0f, (_Float16)-1032.0f});
+                    A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f});
                 }
             }
             const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
@@ -1037,7 +1057,8 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
                 const f4 x0 = QUANT ? acc[m][2 * c] * unscale : acc[m][2 * c];
-                const f4 x1 = QUANT ? acc[m][2 * c + 1] * unscale : acc[m][2 * c + 1];
+                // q4_0 tile 1: 16x its values (exact power of two)
+                const f4 x1 = QUANT ? acc[m][2 * c + 1] * (KT == XQ_TYPE_Q4_0 ? unscale * 0.0625f : unscale) : acc[m][2 * c + 1];
                 if constexpr (KT == XQ_TYPE_Q4_0) {
                     *(f4*)(mw + acc_dim<KT>(c, 0, lg, 0)) = x0;
                     *(f4*)(mw + acc_dim<KT>(c, 1, lg, 0)) = x1;
