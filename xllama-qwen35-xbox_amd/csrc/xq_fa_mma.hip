@@ -111,15 +111,25 @@ struct DecCfg {
     static constexpr bool FITS = SMEM + 2 * NW * NPP * 4 + 64 <= 160 * 1024;
 };
 
-// 8 K bytes (elements 8g..8g+7 of block b) of a q8_0 / q4_0 record in LDS as
-// an int8 MFMA operand. q4_0 elements 0..15 are the low nibbles of bytes
-// 0..15, elements 16..31 the high nibbles; nibble n becomes the signed byte
-// 16*(n - 8) = (n << 4) ^ 0x80.
+// 8 K bytes of block b of a q8_0 / q4_0 record in LDS as an int8 MFMA
+// operand: the block's elements in lane group g's eight k slots. q8_0: elements
+// 8g..8g+7. q4_0 (elements 0..15 are the low nibbles of bytes 0..15, 16..31
+// the high nibbles): the two nibbles of bytes 4g..4g+3, elements 4g..4g+3 then
+// 16+4g..16+4g+3 (the Q operand takes the same order; the block's integer dot
+// does not depend on it); nibble n becomes the signed byte 16*(n - 8) =
+// (n << 4) ^ 0x80.
 template <int KT>
 XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
     constexpr int BB = KT == XQ_TYPE_Q8_0 ? 34 : 18;
-    const int off = KT == XQ_TYPE_Q8_0 ? BB * b + 2 + 8 * g : BB * b + 2 + 8 * (g & 1);
     const int sh = (BB * b + 2) & 3;  // 0 or 2, depends on b only
+    if constexpr (KT == XQ_TYPE_Q4_0) {
+        const int off = BB * b + 2 + 4 * g;
+        const uint32_t w = sh == 0 ? lds_u32(rec + off) : __builtin_amdgcn_alignbyte(lds_u32(rec + off + 2), lds_u32(rec + off - 2), 2);
+        const uint32_t lo = ((w << 4) & 0xf0f0f0f0u) ^ 0x80808080u;
+        const uint32_t hi = (w & 0xf0f0f0f0u) ^ 0x80808080u;
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    }
+    const int off = BB * b + 2 + 8 * g;
     uint32_t w0, w1;
     if (sh == 0) {
         w0 = lds_u32(rec + off);
@@ -128,11 +138,6 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
         const uint32_t x = lds_u32(rec + off - 2), m = lds_u32(rec + off + 2), c = lds_u32(rec + off + 6);
         w0 = __builtin_amdgcn_alignbyte(m, x, 2);
         w1 = __builtin_amdgcn_alignbyte(c, m, 2);
-    }
-    if constexpr (KT == XQ_TYPE_Q4_0) {
-        const int ls = 4 - (g >> 1) * 4;  // low nibbles move to the high half of the byte
-        w0 = ((w0 << ls) & 0xf0f0f0f0u) ^ 0x80808080u;
-        w1 = ((w1 << ls) & 0xf0f0f0f0u) ^ 0x80808080u;
     }
     return (int64_t)(((uint64_t)w1 << 32) | w0);
 }
@@ -555,7 +560,10 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             const uint8_t* img = sQ + (16 * m + lr) * QRB;
 #pragma unroll
             for (int c = 0; c < NB; ++c) {
-                qb[m][c] = *(const int64_t*)(img + 32 * c + 8 * lg);
+                // q4_0: elements 4lg..4lg+3 and 16+4lg..16+4lg+3, K's order
+                qb[m][c] = KT == XQ_TYPE_Q4_0
+                               ? (int64_t)(((uint64_t)lds_u32(img + 32 * c + 16 + 4 * lg) << 32) | lds_u32(img + 32 * c + 4 * lg))
+                               : *(const int64_t*)(img + 32 * c + 8 * lg);
                 if (c % 4 == 0) dqb[m][c / 4] = ((const float*)(img + D))[c + lg];
             }
         }
