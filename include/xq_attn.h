@@ -97,7 +97,8 @@ enum xq_fa_qk_policy {
  * (patches/0008-flash-attn-query-consistency.patch:40-56). Partial states
  * are merged in ascending split order.
  *  XQ_FA_SPLIT_AUTO: MI355X policy, about 256 / (sequences x KV heads) splits
- *    (one workgroup per CU), rows a multiple of 16. It depends on the number
+ *    (one workgroup per CU), rows a multiple of 16 and at least 256 per split
+ *    (at most ceil(L/256) splits). It depends on the number
  *    of sequences and KV heads of the call: a sequence's bits can change with
  *    the batch it is in.
  *  The other modes depend on the KV length only (as the reference's do,

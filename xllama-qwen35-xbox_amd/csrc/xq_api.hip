@@ -101,9 +101,14 @@ void split_policy(int64_t L, int mode, int64_t n_seq_heads, int32_t* n_splits, i
     switch (mode) {
     case XQ_FA_SPLIT_AUTO: {
         // about one workgroup per CU (256 on MI355X) over the (sequence, KV
-        // head) pairs, rows a multiple of the 16-row wave slice
+        // head) pairs, rows a multiple of the 16-row wave slice, and at least
+        // 256 rows per split (two slices per wave of the 8-wave decode): a
+        // short call is bound by latency, and a second slice per wave costs
+        // less than the partial states the extra splits write and merge
+        // (4096 f16 rows over 8 KV heads: 16 splits 15.9 us per call, 32
+        // splits 16.8 us)
         k = cdiv(256, n_seq_heads < 1 ? 1 : n_seq_heads);
-        const int64_t kmax = cdiv(L, 16);
+        const int64_t kmax = cdiv(L, 256);
         if (k > kmax) k = kmax;
         if (k > 256) k = 256;
         if (k < 1) k = 1;
