@@ -869,24 +869,29 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     x[m][i] = seen ? x[m][i] : -INFINITY;
                 }
         }
-        bool grow = false;
-        float mnew[MT];
+        // A pair's maximum moves only when one of its lanes holds a score above
+        // the bound, so the lanes' own maxima are tested first and the
+        // cross-lane reductions run only for a slice where one does (in the
+        // first slices, and rarely after): the same maxima either way
+        float lmax[MT];
+        bool over = false;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const float mt = xrow_max(fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3])));
-            // integer maxima: every rescale factor is an exact power of two and
-            // the pair's power 2^S_p folds exactly into the exponent argument
-            mnew[m] = mt > m_run[m] + kLazyMax ? ceilf(mt) : m_run[m];
-            grow |= mnew[m] != m_run[m];
+            lmax[m] = fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3]));
+            over |= lmax[m] > m_run[m] + kLazyMax;
         }
-        if (__builtin_amdgcn_ballot_w64(grow)) {
+        if (__builtin_amdgcn_ballot_w64(over)) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const float al = mnew[m] == m_run[m] ? 1.0f : __builtin_amdgcn_exp2f(m_run[m] - mnew[m]);
+                const float mt = xrow_max(lmax[m]);
+                // integer maxima: every rescale factor is an exact power of two and
+                // the pair's power 2^S_p folds exactly into the exponent argument
+                const float mnew = mt > m_run[m] + kLazyMax ? ceilf(mt) : m_run[m];
+                const float al = mnew == m_run[m] ? 1.0f : __builtin_amdgcn_exp2f(m_run[m] - mnew);
                 l_run[m] *= al;
 #pragma unroll
                 for (int n = 0; n < 2 * NB; ++n) acc[m][n] *= al;
-                m_run[m] = mnew[m];
+                m_run[m] = mnew;
             }
         }
         // -- quantized V: each pair's largest block-scale exponent over the rows
