@@ -135,3 +135,42 @@ def test_gdn_chunked_magnitude_sweep(torch_gpu, v_scale, bf16):
     rel = np.abs(got[:, :v] - want[:, :v]).max() / np.abs(want[:, :v]).max()
     print(f"v_scale={v_scale} bf16={bf16}: rel {rel:.2e}")
     assert rel <= 1e-4, rel
+
+
+@pytest.mark.parametrize("mode,T", [(xqattn.GDN_STEP, 3), (xqattn.GDN_CHUNKED, 200)], ids=["step", "chunked"])
+def test_gdn_graph_replays_match_eager(torch_gpu, mode, T):
+    """A captured call (the step kernel, or the prep and scan launches of the
+    chunked prefill, as the bench replays them) replays bit-identically, with
+    the output cleared before each replay and eager calls between the replays."""
+    torch = torch_gpu
+    case_note(f"gdn graph replays mode {mode} T {T}")
+    case = make_gdn_case(T, 3, B=2, dist="north_star", seed=23, bf16=True)
+    dev = {n: xqattn.DevTensor.from_host(getattr(case, n)) for n in ("q", "k", "v", "g", "beta", "state")}
+    dst = xqattn.DevTensor.from_host(case.dst)
+    n_ws = xqattn.gated_delta_net_workspace(dev["q"], dev["v"], case.slots, mode)
+    ws = torch.zeros(max(n_ws, 1) + 256, dtype=torch.uint8, device="cuda")
+
+    def call():
+        xqattn.gated_delta_net(dev["q"], dev["k"], dev["v"], dev["g"], dev["beta"], dev["state"], dst,
+                               case.slots, mode=mode, workspace=ws)
+
+    call()
+    torch.cuda.synchronize()
+    eager = dst.to_host_bytes().copy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        call()
+    for rep in range(4):
+        dst.t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.to_host_bytes(), eager), f"replay {rep} differs"
+        call()  # eager work between the replays
+        torch.cuda.synchronize()
+    got = np.frombuffer(eager.tobytes(), np.float32).reshape(case.B, -1, 4096)
+    want = case.oracle_f64()
+    valid = T + 128 * min(T, case.slots)
+    assert_close(got[:, :valid], want[:, :valid], what=f"graph case vs float64 (mode {mode})")
