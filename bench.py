@@ -299,6 +299,46 @@ def summarize_pmc(fetch_dir, write_dir, kernel, workload, copy_bytes, command):
     return rec, "\n".join(lines) + "\n"
 
 
+def copy_ceiling(torch, total_bytes, n_sets, steps, warmup, read_only):
+    """What plain torch kernels take to move `total_bytes` of HBM traffic per
+    call over `n_sets` rotated buffers (beyond the Infinity Cache): a device
+    copy of half the bytes (read + write) and an elementwise pass over them,
+    timed from HIP-graph replays like the op; with read_only, also a
+    reduction that reads all the bytes once (timed eagerly: torch's reduction
+    clears memory inside a graph), the shape of a read-dominated call."""
+    half = total_bytes // 2 // 16 * 16
+    bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda"), torch.empty(half, dtype=torch.uint8, device="cuda"))
+            for _ in range(n_sets)]
+    fbufs = [(a.view(torch.float32), b.view(torch.float32)) for a, b in bufs]
+
+    def copy_call(i):  # the runtime's device-to-device copy
+        bufs[i][1].copy_(bufs[i][0])
+
+    def ew_call(i):  # an elementwise kernel reading and writing the same bytes
+        torch.mul(fbufs[i][0], 1.0, out=fbufs[i][1])
+
+    ceil = {"bytes": 2 * half}
+    for name, fn in (("memcpy", copy_call), ("elementwise", ew_call)):
+        c_stats = {}
+        c_ms, _ = graph_time(torch, fn, n_sets, steps, warmup, c_stats)
+        ceil[name] = {"us_per_call": round(c_ms * 1000, 3), "GB/s": round(2 * half / (c_ms * 1e-3) / 1e9, 1),
+                      "call_us_dist": c_stats}
+        log(f"copy ceiling ({name}): {c_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
+    if read_only:
+        whole = [torch.cat([a, b]).view(torch.float32) for a, b in bufs]  # all the bytes, read once
+        del bufs, fbufs
+        res = torch.empty((), dtype=torch.float32, device="cuda")
+
+        def read_call(i):
+            torch.sum(whole[i], out=res)
+
+        r_ms = time_calls(torch, read_call, n_sets, steps, warmup)
+        ceil["read_sum"] = {"us_per_call": round(r_ms * 1000, 3), "GB/s": round(2 * half / (r_ms * 1e-3) / 1e9, 1)}
+        log(f"read ceiling (sum): {r_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
+        del whole
+    return ceil
+
+
 def kernel_times(torch, xq, fn, n_sets, steps):
     xq.profile_reset()
     xq.profile_enable(True)
@@ -368,7 +408,8 @@ def main():
                     help="run one plain device copy of 512 MiB first (counter calibration for --pmc runs)")
     ap.add_argument("--only", choices=["fa", "gdn", "prefill", "all"], default="all")
     ap.add_argument("--copy-ceiling", action="store_true",
-                    help="also time a plain device copy of the GDN step's bytes (its practical ceiling)")
+                    help="also time plain torch kernels over the FA decode's and the GDN step's bytes "
+                         "(their practical ceilings)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary of --pmc-kernel from two rocprofv3 --pmc output dirs and exit")
     ap.add_argument("--pmc-kernel", choices=["fa_dec", "gdn_step"], default="fa_dec",
@@ -409,11 +450,13 @@ def main():
         log("calibration copy of 512 MiB done")
         del a, b
 
-    # int8 x int8 score dots and f16 x f16 value products on the matrix cores,
+    # int8 x int8 score dots (ggml's exact block dots) and value products with
+    # f32-class operands (weight x block scale as f16 hi + lo, about 22
+    # significant bits, against the exact V values) on the matrix cores;
     # softmax and every accumulation in f32
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-           "dtype": "i8/f16 products, f32 accumulation", "data": "synthetic"}
+           "dtype": "i8 score dots, f32-class (f16 hi+lo) value products, f32 accumulation", "data": "synthetic"}
 
     # ---------------- FA decode @32k q8_0 (headline)
     cfg = wl.FA_C2
@@ -451,7 +494,9 @@ def main():
             "config": {"workload": cfg.name, "op": "GGML_OP_FLASH_ATTN_EXT", "kv_type": "q8_0", "n_q": cfg.n_q,
                        "n_head": cfg.H, "n_head_kv": cfg.Hkv, "head_dim": cfg.D, "kv_len": cfg.L,
                        "n_seq": cfg.B, "mask": "f16 all-visible", "input_sets": n_sets, "timed_calls": n_timed,
-                       "compute": "int8 MFMA q8_0 scores, f16 MFMA values, f32 online softmax and accumulation"},
+                       "compute": "int8 MFMA q8_0 scores (ggml's exact block dots); value products w x d_v as "
+                                  "f16 hi + lo (about 22 significant bits, f32-class) on f16 MFMA against the "
+                                  "exact int8 values; f32 online softmax and accumulation"},
             "us_per_call": round(ms_call * 1000, 2),
             "call_us_dist": call_stats,
             "pct_of_8TBs": round(100 * gbs / PEAK_GBS, 1),
@@ -469,11 +514,17 @@ def main():
             "kernels": kt,
             "kernel_us_dist": {k: dist_ms(v) for k, v in ks.items()},
         })
+        if args.copy_ceiling:
+            # the same bytes through plain torch kernels: 285 MB read (a
+            # reduction) and 285 MB of copy traffic, over the same rotation
+            out["copy_ceiling"] = copy_ceiling(torch, alg, n_sets, args.steps, args.warmup, read_only=True)
 
     # ---------------- the other attention configs: f16 decode at 4k, q4_0 MTP verify
     if args.only in ("fa", "all"):
-        for key, xcfg, comp in (("fa_decode_f16", wl.FA_C1, "f16 MFMA scores (f32 Q as f16 hi + lo) and values"),
-                                ("fa_verify", wl.FA_C5, "int8 MFMA q4_0 scores, f16 MFMA values")):
+        for key, xcfg, comp in (("fa_decode_f16", wl.FA_C1, "f16 MFMA scores (f32 Q as f16 hi + lo) and values "
+                                                             "(weights as f16 hi + lo), f32 accumulation"),
+                                ("fa_verify", wl.FA_C5, "int8 MFMA q4_0 scores, value products w x d_v as f16 "
+                                                        "hi + lo on f16 MFMA, f32 accumulation")):
             x_sets_n = max(2, math.ceil(512 * 2**20 / xcfg.kv_bytes()))
             log(f"building {x_sets_n} input sets of {xcfg.name}")
             xsets = make_fa_sets(torch, xq, wl, xcfg, x_sets_n, seed=3)
@@ -539,38 +590,8 @@ def main():
             # the step moves the state in (17 MB) and out (17 MB) plus 0.4 MB of token
             # inputs and outputs: a device copy of half the algorithmic bytes reads
             # and writes the same amount, on the same rotation of distinct buffers
-            half = g_alg // 2
-            bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda"),
-                     torch.empty(half, dtype=torch.uint8, device="cuda")) for _ in range(g_sets_n)]
-
-            fbufs = [(a.view(torch.float32), b.view(torch.float32)) for a, b in bufs]
-
-            def copy_call(i):  # the runtime's device-to-device copy
-                bufs[i][1].copy_(bufs[i][0])
-
-            def ew_call(i):  # an elementwise kernel reading and writing the same bytes
-                torch.mul(fbufs[i][0], 1.0, out=fbufs[i][1])
-
-            import ctypes
-            probe = ctypes.CDLL(str(ROOT / "xllama-qwen35-xbox_amd" / "xqattn" / "libxqprobe.so"))
-            probe.xqp_stream_copy.restype = ctypes.c_int
-            probe.xqp_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
-            half16 = half // 16 * 16
-
-            def stream_call(i):  # a streaming copy with the step kernel's launch shape
-                st = probe.xqp_stream_copy(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), half16,
-                                           torch.cuda.current_stream().cuda_stream)
-                assert st == 0, st
-
-            ceil = {"bytes": 2 * half}
-            for name, fn in (("memcpy", copy_call), ("elementwise", ew_call), ("stream_copy", stream_call)):
-                c_stats = {}
-                c_ms, _ = graph_time(torch, fn, g_sets_n, max(args.steps, 100), args.warmup, c_stats)
-                ceil[name] = {"us_per_call": round(c_ms * 1000, 3), "GB/s": round(2 * half / (c_ms * 1e-3) / 1e9, 1),
-                              "call_us_dist": c_stats}
-                log(f"copy ceiling ({name}): {c_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
-            out["gdn_step"]["copy_ceiling"] = ceil
-            del bufs, fbufs
+            out["gdn_step"]["copy_ceiling"] = copy_ceiling(torch, g_alg, g_sets_n, max(args.steps, 100),
+                                                           args.warmup, read_only=False)
         if args.only == "gdn":
             out.update({"value": round(g_alg / (g_ms * 1e-3) / 1e9, 1), "unit": "GB/s",
                         "ms_per_step": round(g_ms, 5), "config": {"workload": gcfg.name}})

@@ -113,7 +113,13 @@ enum xq_fa_qk_policy {
  *  XQ_FA_SPLIT_MQ_BALANCED / MQ_FINE: the reference's multi-query verify split
  *    (q4_mq_split, uwp/rkva/rkva-range-profile.h:141-147): the balanced / fine
  *    mode's rows rounded up to whole 64-row tiles, the count recomputed so no
- *    split is empty (58128 rows: 114 x 512 / 228 x 256). */
+ *    split is empty (58128 rows: 114 x 512 / 228 x 256).
+ *  XQ_FA_SPLIT_LENGTH: MI355X length-only split: AUTO's partition evaluated
+ *    for 16 (sequence x KV head) units whatever the call holds, i.e. at most
+ *    16 splits of a multiple of 16 rows, at least 256 rows each. A call with
+ *    16 such units (4 sequences x 4 KV heads at 32k rows, one workgroup per
+ *    CU) runs exactly AUTO's partition; others trade occupancy for results
+ *    that do not depend on the batch. */
 enum xq_fa_split_mode {
     XQ_FA_SPLIT_AUTO = 0,
     XQ_FA_SPLIT_REFERENCE = 1,
@@ -123,13 +129,15 @@ enum xq_fa_split_mode {
     XQ_FA_SPLIT_NONE = 5,
     XQ_FA_SPLIT_MQ_BALANCED = 6,
     XQ_FA_SPLIT_MQ_FINE = 7,
+    XQ_FA_SPLIT_LENGTH = 8,
 };
 
 /* Which pass-1 kernel computes the scores and the value product.
  *  XQ_FA_ENGINE_AUTO: the matrix-core kernel where it exists (q8_0/q4_0 K with
- *    integer scores, F16/E5M2 K), else the VALU kernel. Its quantized-V value
- *    products (weight x block scale) are rounded once to f16 (2^-11 relative
- *    each); F16/E5M2 V weights enter as f16 hi + lo.
+ *    integer scores, F16/E5M2 K), else the VALU kernel. Its value products
+ *    (quantized V: weight x block scale; F16/E5M2 V: the weight) enter the
+ *    matrix cores as f16 hi + lo, about 22 significant bits, against the exact
+ *    V values, with f32 accumulation.
  *  XQ_FA_ENGINE_MFMA: the matrix-core kernel (UNSUPPORTED where it does not exist).
  *  XQ_FA_ENGINE_VALU: the vector-ALU kernel (dot4 integer scores, f32 FMA values:
  *    ggml's f32 value products, slower). */
@@ -234,6 +242,21 @@ xq_status xq_fa_range(const float* q, const int32_t* positions, int32_t n_q, int
  *   out [rows][head_dim], lse [rows] (device); 1 <= head_dim <= 512. */
 xq_status xq_fa_lse_merge(const float* parts_out, const float* parts_lse, int32_t n_parts,
                           int64_t rows, int32_t head_dim, float* out, float* lse, void* stream);
+
+/* The reference's knob semantics for the policy fields (host-side, pure
+ * apart from reading the environment). ggml reads two variables, with exact
+ * values only:
+ *   GGML_FLASH_ATTN_NO_QUERY_TILING=4 -> qk_policy = XQ_FA_QK_CONSISTENT
+ *     (patches/0008-flash-attn-query-consistency.patch:7-9: f32 Q with
+ *     expanded F16 K, scalar queries); =1 -> XQ_FA_QK_NATIVE (scalar queries
+ *     with ggml's own Q conversion, :46-56);
+ *   GGML_FLASH_ATTN_NO_SPLIT_KV=1 -> split_mode = XQ_FA_SPLIT_LENGTH
+ *     (patches/0006-cpu-flash-attn-consistent-kv-reduction.patch:7-11: no
+ *     partition of the KV rows that depends on the batch or the threads;
+ *     here a partition by the KV length only).
+ * The reference's flashattn.txt=2 sets both (uwp/inference-bridge.cpp:887-893).
+ * Absent, empty or other values leave the field as it is. */
+xq_status xq_fa_params_from_env(xq_fa_params* params);
 
 /* Split count the policy picks for a KV length (host-side, pure; AUTO is
  * evaluated for one sequence and one KV head). */

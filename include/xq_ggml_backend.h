@@ -58,14 +58,29 @@ typedef struct xq_ggml_node {
     const xq_tensor* src[XQ_GGML_MAX_SRC];  /* NULL where ggml's src[i] is NULL */
 } xq_ggml_node;
 
-/* Backend-wide choices (NULL = all defaults, which are the reference's
- * consistent query policy and the automatic split, engine and GDN modes). */
+/* Backend-wide choices. NULL = the defaults (the reference's consistent query
+ * policy, the automatic split, engine and GDN modes, GDN from one token) with
+ * the environment's ggml flash-attention knobs applied on top
+ * (xq_fa_params_from_env: GGML_FLASH_ATTN_NO_QUERY_TILING,
+ * GGML_FLASH_ATTN_NO_SPLIT_KV, read once at init).
+ *   fa_split_mode: XQ_FA_SPLIT_AUTO under XQ_FA_QK_CONSISTENT runs
+ *     XQ_FA_SPLIT_LENGTH, a partition by the KV length only, so a sequence's
+ *     bits do not depend on the sequences batched with it, as ggml's CPU loop
+ *     under the reference's consistent mode (flashattn.txt=2 sets
+ *     GGML_FLASH_ATTN_NO_SPLIT_KV=1 with it, uwp/inference-bridge.cpp:887-893).
+ *     Under XQ_FA_QK_NATIVE it is the batch-sized AUTO partition.
+ *   gdn_min_tokens: the fewest tokens a GATED_DELTA_NET node needs to run
+ *     here; 2 leaves single-token decode nodes to the CPU and runs T >= 2 on
+ *     the GPU (the reference's hybrid d3d12_set_gdn_enabled(true, 2),
+ *     src/bridge/ggml_d3d12.cpp:68-71,89, set by d3d12gdn.txt=2,
+ *     uwp/inference-bridge.cpp:901-906); any other value means 1, as there. */
 typedef struct xq_ggml_backend_params {
-    int32_t fa_qk_policy;  /* enum xq_fa_qk_policy */
-    int32_t fa_split_mode; /* enum xq_fa_split_mode */
-    int32_t fa_engine;     /* enum xq_fa_engine */
-    int32_t gdn_mode;      /* enum xq_gdn_mode */
-    int32_t reserved[4];
+    int32_t fa_qk_policy;   /* enum xq_fa_qk_policy */
+    int32_t fa_split_mode;  /* enum xq_fa_split_mode */
+    int32_t fa_engine;      /* enum xq_fa_engine */
+    int32_t gdn_mode;       /* enum xq_gdn_mode */
+    int32_t gdn_min_tokens; /* 1 or 2 */
+    int32_t reserved[3];
 } xq_ggml_backend_params;
 
 typedef struct xq_ggml_backend xq_ggml_backend;
@@ -84,8 +99,15 @@ void* xq_ggml_backend_stream(const xq_ggml_backend* backend);
 size_t xq_ggml_backend_workspace_bytes(const xq_ggml_backend* backend);
 
 /* dev_supports_op (ggml_d3d12.cpp:2331-2353): 1 when graph_compute runs the
- * node (no-op kinds included), 0 otherwise. Pure; needs no GPU. */
+ * node (no-op kinds included), 0 otherwise. Pure; needs no GPU.
+ * xq_ggml_supports_op_params answers for a backend created with these params
+ * (gdn_min_tokens, the FA policy fields; NULL = the defaults without the
+ * environment): the predicate its graph_compute applies, as the reference's
+ * supports_op reads the mode d3d12_set_gdn_enabled set
+ * (ggml_d3d12.cpp:77-109). xq_ggml_supports_op(node) answers for the
+ * defaults. */
 int xq_ggml_supports_op(const xq_ggml_node* node);
+int xq_ggml_supports_op_params(const xq_ggml_node* node, const xq_ggml_backend_params* params);
 
 /* graph_compute (ggml_d3d12.cpp:1836-1942): runs nodes[0 .. n_nodes) in order
  * and returns once they have completed on the device. XQ_ERR_UNSUPPORTED

@@ -61,8 +61,11 @@ def _selftest_inputs(T, B, seed=1701):
     return q, k, v, g, beta, st
 
 
-def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False, v_scale=1.0) -> GdnCase:
-    """v_scale multiplies v and the initial state (the recurrence is linear in them)."""
+def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False, v_scale=1.0,
+                  qk_edit=None) -> GdnCase:
+    """v_scale multiplies v and the initial state (the recurrence is linear in
+    them); qk_edit(q, k) edits the f32 q [B,T,16,128] and k rows in place
+    before they are stored."""
     if dist == "selftest":
         q, k, v, g, beta, st = _selftest_inputs(T, B)
     else:
@@ -70,6 +73,8 @@ def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False
     if v_scale != 1.0:
         v = (v * np.float32(v_scale)).astype(np.float32)
         st = (st * np.float32(v_scale)).astype(np.float32)
+    if qk_edit is not None:
+        qk_edit(q, k)
     typ = wl.BF16 if bf16 else wl.F32
     if bf16:
         q, k, v = (oracle.f32_to_bf16(a) for a in (q, k, v))

@@ -60,16 +60,32 @@ def test_split_policy_reference_known_answers():
     assert (sc(58128, xqattn.SPLIT_MQ_FINE), xqattn.split_rows(58128, xqattn.SPLIT_MQ_FINE)) == (228, 256)
 
 
+def test_split_policy_length_mode():
+    """The length-only mode is AUTO's partition for 16 (sequence x KV head)
+    units: 16 x 2048 rows at 32k (the 4-sequence, 4-KV-head decode's own AUTO
+    partition), 16 x 256 at 4k, 16 x 1040 at 16392, ceil(L/256) splits of 256
+    below 4096 rows, one split up to 256 rows."""
+    sc, sr = xqattn.split_count, xqattn.split_rows
+    L_ = xqattn.SPLIT_LENGTH
+    assert (sc(32768, L_), sr(32768, L_)) == (16, 2048)
+    assert (sc(4096, L_), sr(4096, L_)) == (16, 256)
+    assert (sc(16392, L_), sr(16392, L_)) == (16, 1040)
+    assert (sc(1000, L_), sr(1000, L_)) == (4, 256)
+    assert (sc(256, L_), sr(256, L_)) == (1, 256) and (sc(1, L_), sr(1, L_)) == (1, 16)
+    for L in (1, 17, 255, 4097, 32768, 131072):
+        assert sc(L, L_) <= 16 and sr(L, L_) % 16 == 0 and sr(L, L_) * (sc(L, L_) - 1) < L <= sr(L, L_) * sc(L, L_)
+
+
 @pytest.mark.parametrize("mode", [xqattn.SPLIT_AUTO, xqattn.SPLIT_REFERENCE, xqattn.SPLIT_BALANCED,
                                   xqattn.SPLIT_FINE, xqattn.SPLIT_COARSE, xqattn.SPLIT_NONE,
-                                  xqattn.SPLIT_MQ_BALANCED, xqattn.SPLIT_MQ_FINE])
+                                  xqattn.SPLIT_MQ_BALANCED, xqattn.SPLIT_MQ_FINE, xqattn.SPLIT_LENGTH])
 def test_split_policy_covers_every_row(mode):
     for L in [1, 7, 16, 31, 32, 33, 128, 129, 255, 256, 257, 512, 1000, 4096, 4133, 16392, 28672, 32768, 131072]:
         k = xqattn.split_count(L, mode)
         rows = xqattn.split_rows(L, mode)
         assert 1 <= k <= 256
         assert rows * k >= L, (L, k, rows)  # every row is covered
-        if mode == xqattn.SPLIT_AUTO:
+        if mode in (xqattn.SPLIT_AUTO, xqattn.SPLIT_LENGTH):
             assert rows % 16 == 0 and rows * (k - 1) < L  # no empty split
         if L in (1, 31, 32, 33, 128, 129, 512, 4096, 28672, 131072):
             assert rows * (k - 1) < L  # the reference's own assertion for these lengths

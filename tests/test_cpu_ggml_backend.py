@@ -154,3 +154,52 @@ def test_gdn_contract_flips_of_the_reference_test():
     assert not xqattn.ggml_supports_op(node()) and not direct()
     v.ne[3] = 1
     assert xqattn.ggml_supports_op(node()) and direct()
+
+
+def test_gdn_min_tokens_hybrid_cpu_t1_gpu_t2():
+    """The reference's width cases (tests/test_ggml_d3d12.cpp:273-285): T = 1 and
+    T = 2 nodes (5 slots) both satisfy the full contract with the default
+    minimum; with gdn_min_tokens = 2 (d3d12_set_gdn_enabled(true, 2), the
+    d3d12gdn.txt=2 hybrid) only T = 2 runs here and T = 1 stays on the CPU.
+    Values other than 2 mean 1, as the reference's setter maps them."""
+    for tokens in (1, 2):
+        q, k, v, g, beta, s, dst = _gdn_descs(T=tokens, B=1, slots=5)
+        node = xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, 5)
+        assert xqattn.ggml_supports_op(node)
+        assert xqattn.ggml_supports_op(node, xqattn.backend_params(gdn_min_tokens=1))
+        assert xqattn.ggml_supports_op(node, xqattn.backend_params(gdn_min_tokens=2)) == (tokens == 2)
+        for other in (0, 3, -1):
+            assert xqattn.ggml_supports_op(node, xqattn.backend_params(gdn_min_tokens=other))
+
+
+def test_supports_op_params_rejects_bad_params():
+    q, k, v, g, beta, s, dst = _gdn_descs(T=2, B=1, slots=1)
+    node = xqattn.GgmlNode.gated_delta_net(q, k, v, g, beta, s, dst, 1)
+    assert xqattn.ggml_supports_op(node, xqattn.backend_params())
+    assert not xqattn.ggml_supports_op(node, xqattn.backend_params(gdn_mode=7))
+    assert not xqattn.ggml_supports_op(node, xqattn.backend_params(fa_split_mode=9))
+
+
+@pytest.mark.parametrize("env,want", [
+    ({}, (xqattn.QK_NATIVE, xqattn.SPLIT_BALANCED)),  # absent: unchanged
+    ({"GGML_FLASH_ATTN_NO_QUERY_TILING": "4"}, (xqattn.QK_CONSISTENT, xqattn.SPLIT_BALANCED)),
+    ({"GGML_FLASH_ATTN_NO_QUERY_TILING": "1"}, (xqattn.QK_NATIVE, xqattn.SPLIT_BALANCED)),
+    ({"GGML_FLASH_ATTN_NO_QUERY_TILING": "4 "}, (xqattn.QK_NATIVE, xqattn.SPLIT_BALANCED)),  # exact values only
+    ({"GGML_FLASH_ATTN_NO_SPLIT_KV": "1"}, (xqattn.QK_NATIVE, xqattn.SPLIT_LENGTH)),
+    ({"GGML_FLASH_ATTN_NO_SPLIT_KV": "0"}, (xqattn.QK_NATIVE, xqattn.SPLIT_BALANCED)),
+    ({"GGML_FLASH_ATTN_NO_SPLIT_KV": "11"}, (xqattn.QK_NATIVE, xqattn.SPLIT_BALANCED)),
+    # flashattn.txt=2 (uwp/inference-bridge.cpp:887-893) sets both
+    ({"GGML_FLASH_ATTN_NO_QUERY_TILING": "4", "GGML_FLASH_ATTN_NO_SPLIT_KV": "1"},
+     (xqattn.QK_CONSISTENT, xqattn.SPLIT_LENGTH)),
+])
+def test_fa_params_from_env_knob_semantics(monkeypatch, env, want):
+    """ggml's strict parse of the two knobs (patches/0006-…:9-10,
+    patches/0008-…:7-8,46-50): exactly "4" / "1" and exactly "1"."""
+    for name in ("GGML_FLASH_ATTN_NO_QUERY_TILING", "GGML_FLASH_ATTN_NO_SPLIT_KV"):
+        monkeypatch.delenv(name, raising=False)
+    for name, val in env.items():
+        monkeypatch.setenv(name, val)
+    p = xqattn.fa_params(1 / 16, qk_policy=xqattn.QK_NATIVE, split_mode=xqattn.SPLIT_BALANCED)
+    xqattn.fa_params_from_env(p)
+    assert (p.qk_policy, p.split_mode) == want
+    assert p.scale == pytest.approx(1 / 16) and p.engine == xqattn.ENGINE_AUTO

@@ -11,8 +11,8 @@ sees none has O = 0 and LSE = -inf (uwp/rkva/remote-attn-protocol.h:228-231).
 
 Tolerance: the reference's range-probe bar against the restatement, O within
 3e-4 + 3e-4|ref| and LSE within 3e-4 + 3e-5|ref| (tests/rkva_range_probe.py:139,148);
-against float64, relative to the largest output, 1e-3 for quantized V and 1e-4
-for F16 / E5M2 V, and LSE within 1e-4 + 1e-5|ref|.
+against float64, relative to the largest output, 1e-5 for every KV type, and
+LSE within 1e-4 + 1e-5|ref|.
 """
 import numpy as np
 import pytest
@@ -117,7 +117,6 @@ def test_fa_range_random_shapes(torch_gpu, i):
     if np.any(~empty):
         err = float(np.abs(got - ref64).max())
         rel = err / max(float(np.abs(ref64).max()), 1e-30)
-        bound = 1e-3 if kv in (wl.Q8_0, wl.Q4_0) else 1e-4
-        assert rel < bound, (note, rel)
+        assert rel < 1e-5, (note, rel)
         assert_close(glse[~empty], lse64[~empty], atol=1e-4, rtol=1e-5, what=f"{note} LSE vs float64")
         print(f"{note}: max|gpu-f64| / max|f64| {rel:.2e}")

@@ -119,6 +119,54 @@ def test_gdn_chunked_strong_decay(torch_gpu):
 
 
 
+def _q_large(q, k):
+    q[:, 100:110, 3] *= np.float32(1e5)  # |q| |k| per element far above 256: f16 P tiles would overflow
+
+
+def _k_large(q, k):
+    k[:, 200, 5] *= np.float32(100.0)  # |k| above 16
+
+
+def _k_nan(q, k):
+    k[:, 150, 2, 7] = np.float32(np.nan)
+
+
+@pytest.mark.parametrize("pad", [0, 3])
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("edit", [_q_large, _k_large, _k_nan], ids=["q_large", "k_large", "k_nan"])
+def test_gdn_chunked_out_of_range_qk_runs_the_sequential_recurrence(torch_gpu, edit, bf16, pad):
+    """q / k rows outside the range the chunked form's f16 operands hold (the
+    prep's per-chunk check: |k| < 16, |q| < 2^15, |q| |k| < 256, finite) send
+    their (sequence, v-head) through the token-by-token f32 recurrence, so the
+    result is the sequential form's: within the reference selftest's 1e-4 of
+    the float64 recurrence (relative to the largest output) for large rows,
+    and NaN exactly where the restated recurrence has it for a NaN k element
+    (every later token and the final state of the two v-heads on that k-head)."""
+    case_note(f"gdn chunked out-of-range {edit.__name__} bf16={bf16} pad={pad}")
+    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=bf16, seed=5, pad=pad, qk_edit=edit)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    v = _valid_rows(case)
+    if edit is _k_nan:
+        want = case.oracle()
+        assert np.array_equal(np.isnan(got[:, :v]), np.isnan(want[:, :v])), "NaN pattern differs"
+        assert np.isnan(want[:, 150:300, 2 * 128:3 * 128]).all() and not np.isnan(want[:, :150]).any()
+        _check(case, got, want, "NaN k vs restated recurrence")
+        return
+    want = case.oracle_f64()
+    assert np.all(np.isfinite(got[:, :v]))
+    # per v-head (outputs and state of each head apart): the enlarged rows
+    # dominate their own heads' magnitudes only
+    def heads(x):  # [B, 32, ...]: each head's outputs and final state
+        T = case.T
+        y = x[:, :T].reshape(case.B, T, 32, 128).transpose(0, 2, 1, 3).reshape(case.B, 32, -1)
+        st = x[:, T:v].reshape(case.B, 32, -1)  # state (i, c) of head h at h * 16384 + c * 128 + i
+        return np.concatenate([y, st], axis=2)
+    gh, wh = heads(got), heads(want)
+    rel = (np.abs(gh - wh).max(axis=(0, 2)) / np.abs(wh).max(axis=(0, 2))).max()
+    print(f"{edit.__name__} bf16={bf16} pad={pad}: largest per-head rel {rel:.2e}")
+    assert rel <= 1e-4, rel
+
+
 @pytest.mark.parametrize("bf16", [True, False])
 @pytest.mark.parametrize("v_scale", [1e-6, 1e-3, 1e3, 1e6])
 def test_gdn_chunked_magnitude_sweep(torch_gpu, v_scale, bf16):

@@ -61,7 +61,8 @@ def test_graph_fa_and_gdn_match_direct_calls(torch_gpu):
         got_fa = dst_array(fa, d_graph.to_host_bytes())
         got_gdn = out_array(gdn, g_graph.to_host_bytes())
 
-    xqattn.flash_attn_ext(q, k, v, m, None, d_direct, xqattn.fa_params(fa.scale))
+    # the backend's consistent default runs the length-only split
+    xqattn.flash_attn_ext(q, k, v, m, None, d_direct, xqattn.fa_params(fa.scale, split_mode=xqattn.SPLIT_LENGTH))
     xqattn.gated_delta_net(dev["q"], dev["k"], dev["v"], dev["g"], dev["beta"], dev["state"], g_direct, 1)
     torch_gpu.cuda.synchronize()
     assert np.array_equal(got_fa, dst_array(fa, d_direct.to_host_bytes()))
@@ -150,3 +151,54 @@ def test_graph_workspace_grows_once(torch_gpu):
         _run(be, [_gdn_node(sdev, sdst, 1)], torch_gpu)
         assert be.workspace_bytes == need
         assert_close(out_array(step, sdst.to_host_bytes()), step.oracle(), what="step node vs oracle")
+
+
+def test_graph_consistent_default_is_batch_invariant(torch_gpu):
+    """Under the backend's defaults (consistent query policy, automatic split)
+    a sequence's FA output is bitwise the same alone and in a batch of four:
+    the split is the length-only partition (at 32k rows with 4 KV heads the
+    batch-sized AUTO partition would give the lone sequence 64 splits and the
+    batch 16)."""
+    cfg = wl.FaConfig("fa_bi_q4_0_h16kv4_d128_L32768_b4", 2, 16, 4, 128, 32768, 4, wl.Q4_0, causal_prefix=32766)
+    case_note(f"ggml graph: batch invariance {cfg.name}")
+    assert xqattn.split_count(32768, xqattn.SPLIT_LENGTH) == 16
+    fa = make_fa_case(cfg, seed=41, mask_per_seq=True)
+    B, NQ, H, D = fa.shape
+    rec = wl.record_bytes(wl.Q4_0, D)
+    q, k, v, m = (xqattn.DevTensor.from_host(t) for t in (fa.q, fa.k, fa.v, fa.mask))
+    d4 = xqattn.DevTensor.empty_like_host(fa.dst)
+    b = 2
+    q_all = np.frombuffer(fa.q.buf.tobytes(), np.float32).reshape(B, NQ, H, D)
+    m_all = np.frombuffer(fa.mask.buf.tobytes(), np.uint16).reshape(B, fa.mask.ne[1], cfg.L)
+    q1 = xqattn.DevTensor.from_host(wl.fa_q_tensor(q_all[b:b + 1].copy()))
+    k1, v1 = (xqattn.DevTensor.from_host(wl.kv_tensor(t.buf.reshape(B, cfg.L, cfg.Hkv, rec)[b:b + 1].copy(),
+                                                       wl.Q4_0, D)) for t in (fa.k, fa.v))
+    m1 = xqattn.DevTensor.from_host(wl.mask_tensor(m_all[b:b + 1].copy()))
+    d1 = xqattn.DevTensor.empty_like_host(wl.fa_dst_tensor(1, NQ, H, D))
+    with xqattn.GgmlBackend() as be:
+        _run(be, [xqattn.GgmlNode.flash_attn_ext(q, k, v, m, None, d4, fa.scale),
+                  xqattn.GgmlNode.flash_attn_ext(q1, k1, v1, m1, None, d1, fa.scale)], torch_gpu)
+    got4 = np.frombuffer(d4.to_host_bytes().tobytes(), np.float32).reshape(B, NQ, H, D)
+    got1 = np.frombuffer(d1.to_host_bytes().tobytes(), np.float32).reshape(1, NQ, H, D)
+    assert np.array_equal(got1[0].view(np.uint32), got4[b].view(np.uint32)), "sequence 2 alone differs"
+
+
+def test_graph_gdn_min_tokens_two_leaves_single_token_nodes_to_the_cpu(torch_gpu):
+    """With gdn_min_tokens = 2 (the reference's d3d12gdn.txt=2 hybrid) a
+    single-token GDN node is outside the backend's contract: the graph fails
+    before any launch; a two-token node runs."""
+    case_note("ggml graph: gdn_min_tokens 2")
+    one = make_gdn_case(1, 1, B=1, dist="north_star", seed=43)
+    two = make_gdn_case(2, 1, B=1, dist="north_star", seed=44)
+    d1, d2 = _dev_gdn(one), _dev_gdn(two)
+    o1, o2 = xqattn.DevTensor.from_host(one.dst), xqattn.DevTensor.from_host(two.dst)
+    sentinel = o1.to_host_bytes().copy()
+    p = xqattn.backend_params(gdn_min_tokens=2)
+    assert not xqattn.ggml_supports_op(_gdn_node(d1, o1, 1), p) and xqattn.ggml_supports_op(_gdn_node(d2, o2, 1), p)
+    with xqattn.GgmlBackend(gdn_min_tokens=2) as be:
+        with pytest.raises(xqattn.XqError) as e:
+            _run(be, [_gdn_node(d2, o2, 1), _gdn_node(d1, o1, 1)], torch_gpu)
+        assert e.value.status == 1 and "node 1" in str(e.value)
+        assert np.array_equal(o1.to_host_bytes(), sentinel)
+        _run(be, [_gdn_node(d2, o2, 1)], torch_gpu)
+    assert_close(out_array(two, o2.to_host_bytes()), two.oracle(), what="T=2 node with min tokens 2")

@@ -2,7 +2,11 @@
 nothing (its workspace is the library's per-GPU scratch array). It must give
 xq_flash_attn_ext's results bit for bit, on consecutive calls that reuse the
 scratch (the second smaller than the first), and reject a call whose workspace
-exceeds the scratch before launching anything.
+exceeds the scratch before launching anything. Its callers capture HIP graphs:
+the process's first call (which looks the scratch address up) is made under
+capture, and the graph's replays equal the workspace entry's result bit for
+bit, with eager calls between the replays. The capture test comes first in
+this file so that it makes the first call of its process.
 """
 import ctypes
 
@@ -30,6 +34,38 @@ def _run_noalloc(case, torch, split_mode, engine):
     xqattn.flash_attn_ext_noalloc(q, k, v, m, None, d, p, lse=lse)
     torch.cuda.synchronize()
     return dst_array(case, d.to_host_bytes()), lse.cpu().numpy().reshape(B, NQ, H)
+
+
+def test_fa_noalloc_first_call_under_graph_capture_replays_bit_exact(torch_gpu):
+    torch = torch_gpu
+    cfg = wl.FaConfig("na_graph", 2, 24, 4, 256, 5000, 2, wl.Q8_0, causal_prefix=4998)
+    case_note("no-alloc call under graph capture")
+    case = make_fa_case(cfg, seed=19)
+    want, wlse = run_fa_gpu(case, torch, split_mode=xqattn.SPLIT_AUTO, engine=xqattn.ENGINE_AUTO)
+    q, k, v = (xqattn.DevTensor.from_host(t) for t in (case.q, case.k, case.v))
+    m = xqattn.DevTensor.from_host(case.mask)
+    d = xqattn.DevTensor.empty_like_host(case.dst)
+    B, NQ, H, D = case.shape
+    lse = torch.empty(B * NQ * H, dtype=torch.float32, device="cuda")
+    p = xqattn.fa_params(case.scale)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        xqattn.flash_attn_ext_noalloc(q, k, v, m, None, d, p, lse=lse, stream=s)
+    for rep in range(4):
+        d.t.zero_()
+        lse.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = dst_array(case, d.to_host_bytes())
+        glse = lse.cpu().numpy().reshape(B, NQ, H)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"replay {rep}: output differs"
+        assert np.array_equal(glse.view(np.uint32), wlse.view(np.uint32)), f"replay {rep}: LSE differs"
+        xqattn.flash_attn_ext_noalloc(q, k, v, m, None, d, p, lse=lse)  # eager work on the same scratch
+        torch.cuda.synchronize()
 
 
 CALLS = [

@@ -4,6 +4,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -137,6 +138,8 @@ void split_policy(int64_t L, int mode, int64_t n_seq_heads, int32_t* n_splits, i
         k = cdiv(L, r);
         break;
     }
+    // AUTO's partition for 16 (sequence x KV head) units, whatever the call
+    case XQ_FA_SPLIT_LENGTH: split_policy(L, XQ_FA_SPLIT_AUTO, 16, n_splits, rows); return;
     case XQ_FA_SPLIT_NONE:
     default: r = L; k = 1; break;
     }
@@ -165,7 +168,7 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
         return fail(XQ_ERR_UNSUPPORTED, "k/v type %d/%d not supported (F16, Q8_0, Q4_0, E5M2; same type)", k->type, v->type);
     if (p->qk_policy != XQ_FA_QK_CONSISTENT && p->qk_policy != XQ_FA_QK_NATIVE)
         return fail(XQ_ERR_BAD_ARG, "bad qk_policy %d", p->qk_policy);
-    if (p->split_mode < XQ_FA_SPLIT_AUTO || p->split_mode > XQ_FA_SPLIT_MQ_FINE)
+    if (p->split_mode < XQ_FA_SPLIT_AUTO || p->split_mode > XQ_FA_SPLIT_LENGTH)
         return fail(XQ_ERR_BAD_ARG, "bad split_mode %d", p->split_mode);
     if (p->engine < XQ_FA_ENGINE_AUTO || p->engine > XQ_FA_ENGINE_VALU)
         return fail(XQ_ERR_BAD_ARG, "bad engine %d", p->engine);
@@ -250,6 +253,22 @@ int32_t xq_abi_version(void) { return XQ_ABI_VERSION; }
 
 const char* xq_last_error(void) { return g_last_error.c_str(); }
 
+// getenv value equal to want exactly (ggml's strict parse)
+static bool env_is(const char* name, const char* want) {
+    const char* v = getenv(name);
+    return v && strcmp(v, want) == 0;
+}
+
+xq_status xq_fa_params_from_env(xq_fa_params* p) {
+    if (!p) return fail(XQ_ERR_BAD_ARG, "params is null");
+    if (env_is("GGML_FLASH_ATTN_NO_QUERY_TILING", "4"))
+        p->qk_policy = XQ_FA_QK_CONSISTENT;
+    else if (env_is("GGML_FLASH_ATTN_NO_QUERY_TILING", "1"))
+        p->qk_policy = XQ_FA_QK_NATIVE;
+    if (env_is("GGML_FLASH_ATTN_NO_SPLIT_KV", "1")) p->split_mode = XQ_FA_SPLIT_LENGTH;
+    return ok();
+}
+
 int32_t xq_fa_split_count(int64_t kv_len, int32_t split_mode) {
     int32_t n;
     int64_t r;
@@ -327,7 +346,10 @@ xq_status xq_flash_attn_ext(const xq_tensor* q, const xq_tensor* k, const xq_ten
 }
 
 // The scratch array's address on the current device, looked up once per device
-// (with that device current) and kept.
+// (with that device current) and kept. The lookup enqueues no work, but it may
+// load the library's code object onto the device: it runs with this thread's
+// stream-capture mode relaxed, so a first call made while a caller captures a
+// HIP graph (the callers this entry point is for) is legal and is not recorded.
 static hipError_t scratch_address(void** out) {
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
@@ -338,9 +360,14 @@ static hipError_t scratch_address(void** out) {
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(mu);
     if (!addr[dev]) {
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return e;
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);  // restore the caller's mode
         if (e != hipSuccess) return e;
+        if (e2 != hipSuccess) return e2;
         addr[dev] = p;
     }
     *out = addr[dev];

@@ -32,15 +32,18 @@
 //           the B operand, so the softmax weights never leave registers and
 //           every per-pair quantity (maximum, sum, rescale factor) is
 //           lane-local.
-//           q8_0 / q4_0 V: v_mfma_f32_16x16x16_f16 on the exact integer values
+//           q8_0 / q4_0 V: v_mfma_f32_16x16x32_f16 on the exact integer values
 //           as f16 (q4_0's high nibbles as 16x theirs, undone exactly at the
-//           merge) against w * 2^S_p * d_v, each product formed in f32 by one
-//           v_fma_mix and rounded once to f16. 2^S_p, a power of two per pair
-//           sized from the block scales the pair has seen, keeps every product
-//           in f16's normal range whatever V's scale (a product w * d_v would
-//           fall into subnormals, and then to zero, as V's magnitude shrinks);
-//           it enters the weights' exponent argument and leaves at the merge,
-//           both exactly.
+//           merge), the four rows repeated, against w * 2^S_p * d_v as f16
+//           high + low parts: each product formed in f32 by v_fma_mix, its f16
+//           rounding h and the remainder w * 2^S_p * d_v - h as f16, about 22
+//           significant bits (ggml multiplies the weight by the f32 dequantized
+//           value, one f32 rounding). 2^S_p, a power of two per pair sized from
+//           the block scales the pair has seen, keeps every high part in f16's
+//           normal range whatever V's scale (a product w * d_v would fall into
+//           subnormals, and then to zero, as V's magnitude shrinks); it enters
+//           the weights' exponent argument and leaves at the merge, both
+//           exactly.
 //           F16 / E5M2 V: v_mfma_f32_16x16x32_f16 on the exact f16 V against
 //           the weight as f16 high + low parts (products 8lg..8lg+3 of a lane
 //           group: its four rows' high parts, 8lg+4..8lg+7: their low parts;
@@ -54,12 +57,15 @@
 // Rows a pair does not see (mask -inf, past its causal limit or the split)
 // never touch its state, as ggml's loop skips them: a slice that holds such a
 // row or a non-finite score runs "careful" — the scores of unseen rows become
-// -inf whatever K holds, the weight x scale products of quantized V's unseen
-// rows are masked to +0 whatever their scale holds, and non-finite F16/E5M2 V
-// elements are replaced
-// by 0 in the shared V operand while every pair that sees such a row gets a
-// NaN state. Range calls (positions) additionally turn a row whose output or
-// normaliser is not finite into NaN in full (the split reducer's poisoning).
+// -inf whatever K holds, and the weight x scale products of quantized V's
+// unseen rows are masked to +0 whatever their scale holds. Non-finite V
+// reaches exactly the dims it sits in, of the pairs that see its row, as in
+// ggml's per-dim accumulation: F16/E5M2 V elements that are Inf/NaN enter the
+// shared V operand as 0 and are added to those accumulator elements after
+// the products (every slice scans its V rows), and an Inf/NaN block scale's
+// product keeps a zero low part. Range calls (positions) additionally turn a
+// row whose output or normaliser is not finite into NaN in full (the split
+// reducer's poisoning).
 #include <type_traits>
 
 #include "xq_fa_common.h"
@@ -163,27 +169,39 @@ XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32
 }
 
 // B operand of a quantized-V value product: the f32 weights w0..w3 (rows 0..3)
-// times the rows' f16 block scales, each formed in f32 by v_fma_mix and
-// rounded once to f16, packed as rows (0,1) and (2,3). The scale of row i is
+// times the rows' f16 block scales as f16 high + low parts. Each product w*d
+// is formed in f32 by v_fma_mix and rounded to f16 (the high part h); the low
+// part is the remainder w*d - h, formed by one more v_fma_mix from the same
+// operands with -h as the addend and rounded to f16, so h + l holds about 22
+// significant bits of w*d (h is within 2^-11 of w*d). Packed as rows
+// (0,1), (2,3) of the high parts, then of the low parts. The scale of row i is
 // the low (HI = false) or high half of d[i]. s_nop as in q8_vt_f16.
 template <bool HI>
-XQ_DEV void wd_f16(float w0, float w1, float w2, float w3, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
-                   uint32_t& b01, uint32_t& b23) {
+XQ_DEV void wd_f16x2(float w0, float w1, float w2, float w3, uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                     uint32_t& b01, uint32_t& b23, uint32_t& l01, uint32_t& l23) {
     if constexpr (HI)
-        asm("v_fma_mixlo_f16 %0, %2, %6, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixhi_f16 %0, %3, %7, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixlo_f16 %1, %4, %8, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixhi_f16 %1, %5, %9, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+        asm("v_fma_mixlo_f16 %0, %4, %8, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %0, %5, %9, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %1, %6, %10, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %1, %7, %11, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %2, %4, %8, -%0 op_sel:[0,1,0] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixhi_f16 %2, %5, %9, -%0 op_sel:[0,1,1] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixlo_f16 %3, %6, %10, -%1 op_sel:[0,1,0] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixhi_f16 %3, %7, %11, -%1 op_sel:[0,1,1] op_sel_hi:[0,1,1]\n\t"
             "s_nop 1"
-            : "=&v"(b01), "=&v"(b23)
+            : "=&v"(b01), "=&v"(b23), "=&v"(l01), "=&v"(l23)
             : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(d0), "v"(d1), "v"(d2), "v"(d3));
     else
-        asm("v_fma_mixlo_f16 %0, %2, %6, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixhi_f16 %0, %3, %7, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixlo_f16 %1, %4, %8, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
-            "v_fma_mixhi_f16 %1, %5, %9, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+        asm("v_fma_mixlo_f16 %0, %4, %8, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %0, %5, %9, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %1, %6, %10, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixhi_f16 %1, %7, %11, 0 op_sel:[0,0,0] op_sel_hi:[0,1,0]\n\t"
+            "v_fma_mixlo_f16 %2, %4, %8, -%0 op_sel:[0,0,0] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixhi_f16 %2, %5, %9, -%0 op_sel:[0,0,1] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixlo_f16 %3, %6, %10, -%1 op_sel:[0,0,0] op_sel_hi:[0,1,1]\n\t"
+            "v_fma_mixhi_f16 %3, %7, %11, -%1 op_sel:[0,0,1] op_sel_hi:[0,1,1]\n\t"
             "s_nop 1"
-            : "=&v"(b01), "=&v"(b23)
+            : "=&v"(b01), "=&v"(b23), "=&v"(l01), "=&v"(l23)
             : "v"(w0), "v"(w1), "v"(w2), "v"(w3), "v"(d0), "v"(d1), "v"(d2), "v"(d3));
 }
 
@@ -202,6 +220,8 @@ XQ_DEV uint32_t f16x2_zero_nonfinite(uint32_t w) {
 
 // Nonzero when any f16 half of w is Inf or NaN.
 XQ_DEV uint32_t f16x2_nonfinite(uint32_t w) { return ((w & 0x7c007c00u) + 0x04000400u) & 0x80008000u; }
+// 0xffff in each f16 half of w that is finite, 0 in each Inf/NaN half.
+XQ_DEV uint32_t f16x2_finite_mask(uint32_t w) { return ~((f16x2_nonfinite(w) >> 15) * 0xffffu); }
 // Nonzero when any E5M2 byte of w is Inf or NaN.
 XQ_DEV uint32_t e5m2x4_nonfinite(uint32_t w) { return ((w & 0x7c7c7c7cu) + 0x04040404u) & 0x80808080u; }
 
@@ -656,7 +676,9 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     //      their low parts (the V operand repeats the four rows)
     //      pw: f32 weights (row 4lg + i, pair 16m + lr; quantized V: times
     //      2^S_p); seenm: careful slice's masks of the rows the pair sees;
-    //      Bf: F16/E5M2 weight operands; vsan: V sanitising
+    //      Bf: F16/E5M2 weight operands; vsan: F16/E5M2: Inf/NaN V elements
+    //      enter the shared operand as 0; q8_0/q4_0: an Inf/NaN scale's product
+    //      keeps a zero low part
     auto values = [&](auto st_tag, int c, const float (&pw)[MT][4], auto careful_tag, const uint32_t (&seenm)[MT][2],
                       const h8 (&Bf)[MT], bool vsan) {
         constexpr int ST = decltype(st_tag)::value;
@@ -686,25 +708,35 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             }
         }
         if constexpr (QUANT) {
-            // B: w * 2^S * d_v rounded once to f16 (rows (0,1), (2,3)); the
-            // wave's power of two 2^S keeps every product in f16's normal range
+            // B: w * 2^S * d_v as f16 high + low parts (products 8lg..8lg+3 of a
+            // lane group: rows 0..3's high parts, 8lg+4..8lg+7: their low parts);
+            // the pair's power of two 2^S keeps every high part in f16's normal
+            // range
             uint32_t dvw[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
             const bool dhi = ((BB * c) & 2) != 0;  // the scale sits in the high half of its dword
-            h4 Bv[MT];
+            h8 Bv[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                uint32_t b01, b23;
+                uint32_t b01, b23, l01, l23;
                 if (dhi)
-                    wd_f16<true>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
+                    wd_f16x2<true>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23, l01, l23);
                 else
-                    wd_f16<false>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23);
+                    wd_f16x2<false>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23, l01, l23);
+                if (vsan) {
+                    // an Inf/NaN scale: the low part of its product (Inf - Inf)
+                    // is set to 0, so the high part alone gives q * d's Inf / NaN
+                    l01 &= f16x2_finite_mask(b01);
+                    l23 &= f16x2_finite_mask(b23);
+                }
                 if constexpr (careful) {  // rows the pair does not see add 0, whatever their scale holds
                     b01 &= seenm[m][0];
                     b23 &= seenm[m][1];
+                    l01 &= seenm[m][0];
+                    l23 &= seenm[m][1];
                 }
-                Bv[m] = __builtin_bit_cast(h4, uint2{b01, b23});
+                Bv[m] = __builtin_bit_cast(h8, uint4{b01, b23, l01, l23});
             }
             // A: the integer values of tile t's dims in rows (0,1), (2,3) as f16 (exact)
             uint32_t A0[2], A1[2];
@@ -724,12 +756,13 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f});
                 }
             }
-            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
-            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
+            // the four rows repeated: once against the high parts, once against the low
+            const h8 At0 = __builtin_bit_cast(h8, uint4{A0[0], A0[1], A0[0], A0[1]});
+            const h8 At1 = __builtin_bit_cast(h8, uint4{A1[0], A1[1], A1[0], A1[1]});
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
-                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
             }
         } else {
             // A: f16 pairs of rows (0,1), (2,3) of tiles t = 0, 1 (exact)
@@ -831,15 +864,21 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         __builtin_amdgcn_wave_barrier();
         // quantized V: lane l reads the block scales of row l/4 (largest exponent
         // field er), used after the softmax
+        // (dsan: some block scale of the slice is Inf/NaN)
         int er = 0;
+        bool dsan = false;
         if constexpr (QUANT) {
             const uint8_t* vr = ring + S * 2 * SLICE + SLICE + (lane >> 2) * REC;
+            uint32_t hs;
             if constexpr (NB == 8) {
                 const int b0 = 2 * (lane & 3);
-                er = max(scale_exp(lds_u16(vr + BB * b0)), scale_exp(lds_u16(vr + BB * (b0 + 1))));
+                hs = lds_u16(vr + BB * b0) | (lds_u16(vr + BB * (b0 + 1)) << 16);
+                er = max(scale_exp(hs & 0xffffu), scale_exp(hs >> 16));
             } else {
-                er = scale_exp(lds_u16(vr + BB * (lane & 3)));
+                hs = lds_u16(vr + BB * (lane & 3));
+                er = scale_exp(hs);
             }
+            dsan = __builtin_amdgcn_ballot_w64(f16x2_nonfinite(hs) != 0) != 0;
         }
         // -- online softmax (base 2)
         float x[MT][4];
@@ -982,54 +1021,111 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 }
             }
         }
-        // -- careful F16/E5M2 slice: a non-finite V element must not reach the
-        //    pairs that do not see its row through the shared V operand. Lane
-        //    (lr, lg) scans its sixteenth of rows 4lg..4lg+3; if any element is
-        //    Inf/NaN, the V operands are sanitised and each pair that sees a bad
-        //    row gets a NaN sum (its output becomes NaN, as ggml's would)
+        // -- F16/E5M2 V: a non-finite element must reach exactly its own dim of
+        //    the pairs that see its row, as ggml's per-dim accumulation does
+        //    (VKQ += v * vs). It must not reach the pairs that do not see the
+        //    row through the shared V operand, and Inf times a weight's low
+        //    part could give NaN where the product is Inf. Lane (lr, lg) scans
+        //    its sixteenth of rows 4lg..4lg+3 (0 * x is +-0 for finite x, NaN
+        //    otherwise); when any element is Inf/NaN the V operands are
+        //    sanitised and the bad elements are added after the products
         bool vsan = false;
+        uint32_t rowbad = 0;  // rows of the slice holding a non-finite V element (vsan only)
         if constexpr (!QUANT) {
-            if (careful) {
-                constexpr int ES = KT == XQ_TYPE_F16 ? 2 : 1;
-                constexpr int SPAN = ES * D / 16;  // bytes per lane per row (8..32)
-                const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
-                int rb = 0;
+            constexpr int ES = KT == XQ_TYPE_F16 ? 2 : 1;
+            constexpr int SPAN = ES * D / 16;  // bytes per lane per row (8..32)
+            const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
+            uint32_t rb = 0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint8_t* vr = Vs + (4 * lg + i) * REC + lr * SPAN;
-                    uint32_t bad = 0;
+            for (int i = 0; i < 4; ++i) {
+                const uint8_t* vr = Vs + (4 * lg + i) * REC + lr * SPAN;
+                uint32_t bad = 0;
+                if constexpr (KT == XQ_TYPE_F16) {
+                    h2 z = h2{(_Float16)0.0f, (_Float16)0.0f};
 #pragma unroll
-                    for (int k = 0; k < SPAN / 4; ++k) {
-                        const uint32_t w = lds_u32(vr + 4 * k);
-                        bad |= KT == XQ_TYPE_F16 ? f16x2_nonfinite(w) : e5m2x4_nonfinite(w);
+                    for (int k = 0; k < SPAN / 16; ++k) {
+                        const uint4 w = *(const uint4*)(vr + 16 * k);
+                        const h2 zero = h2{(_Float16)0.0f, (_Float16)0.0f};
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.x), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.y), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.z), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.w), zero, z);
                     }
-                    rb |= bad ? 1 << i : 0;
-                }
-                rb |= dpp_i<0xB1>(rb);
-                rb |= dpp_i<0x4E>(rb);
-                rb |= dpp_i<0x141>(rb);
-                rb |= dpp_i<0x140>(rb);  // every lane of the row group: the flags of its four rows
-                vsan = __builtin_amdgcn_ballot_w64(rb != 0) != 0;
-                if (vsan) {
+                    bad = __builtin_bit_cast(uint32_t, z) & 0x7fff7fffu;
+                } else {
 #pragma unroll
-                    for (int m = 0; m < MT; ++m)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (((rb >> i) & 1) && x[m][i] != -INFINITY) l_run[m] = NAN;
+                    for (int k = 0; k < SPAN / 8; ++k) {
+                        const uint2 w = *(const uint2*)(vr + 8 * k);
+                        bad |= e5m2x4_nonfinite(w.x) | e5m2x4_nonfinite(w.y);
+                    }
                 }
+                rb |= bad ? 1u << i : 0u;
+            }
+            vsan = __builtin_amdgcn_ballot_w64(rb != 0) != 0;
+            if (vsan) {
+                rb |= (uint32_t)dpp_i<0xB1>((int)rb);
+                rb |= (uint32_t)dpp_i<0x4E>((int)rb);
+                rb |= (uint32_t)dpp_i<0x141>((int)rb);
+                rb |= (uint32_t)dpp_i<0x140>((int)rb);  // every lane of the row group: the flags of its four rows
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) rowbad |= (uint32_t)__builtin_amdgcn_readlane((int)rb, 16 * g4) << (4 * g4);
             }
         }
         if constexpr (QUANT) {
             if (careful) {
 #pragma unroll
-                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::true_type{}, seenmask, Bf, vsan);
+                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::true_type{}, seenmask, Bf, dsan);
             } else {
 #pragma unroll
-                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::false_type{}, seenmask, Bf, vsan);
+                for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::false_type{}, seenmask, Bf, dsan);
             }
         } else {
 #pragma unroll
             for (int c = 0; c < NB; ++c) values(stage_tag, c, pw, std::false_type{}, seenmask, Bf, vsan);
+            if (vsan) {
+                // the bad elements of each bad row j: pair 16m + lr adds w * v to
+                // its accumulator element of that dim when it sees row j (its
+                // weight comes from lane (lr, j/4), register j % 4); the lane
+                // holds dims 32c + 8lg + 2i + t in acc[m][2c + t][i]
+                float ws[MT][4];
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ws[m][i] = x[m][i] != -INFINITY ? pw[m][i] : -1.0f;
+                const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
+                for (int j = 0; j < kSub; ++j) {
+                    if (!((rowbad >> j) & 1u)) continue;
+                    const int src = lr + 16 * (j >> 2), ji = j & 3;
+                    float wj[MT];
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const float sel = ji == 0 ? ws[m][0] : ji == 1 ? ws[m][1] : ji == 2 ? ws[m][2] : ws[m][3];
+                        wj[m] = __shfl(sel, src);
+                    }
+                    const uint8_t* vr = Vs + j * REC;
+#pragma unroll
+                    for (int c = 0; c < NB; ++c) {
+                        float v[8];
+                        if constexpr (KT == XQ_TYPE_F16) {
+                            const h8 hv = *(const h8*)(vr + 2 * (32 * c + 8 * lg));
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) v[e] = (float)hv[e];
+                        } else {
+                            const uint2 w = *(const uint2*)(vr + 32 * c + 8 * lg);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e)
+                                v[e] = f16_bits_to_f32((((e < 4 ? w.x : w.y) >> (8 * (e & 3))) & 0xffu) << 8);
+                        }
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            if (__builtin_isfinite(v[e])) continue;
+#pragma unroll
+                            for (int m = 0; m < MT; ++m)
+                                if (wj[m] >= 0.0f) acc[m][2 * c + (e & 1)][e >> 1] += wj[m] * v[e];
+                        }
+                    }
+                }
+            }
         }
 
         // -- the V unit of slice j+2 into the stage this slice's V used

@@ -61,11 +61,14 @@
 // |v| of the column block over the prefill and the largest |S| entering it so
 // that they lie in [1, 2), and divides Y and the final state by 2^a (exact). V
 // and the state may so have any f32 magnitude: f16's range holds a state that
-// grows 2^15-fold beyond them. q and k rows enter as f16 (or hi + lo): they
-// must lie in the L2-normalised range the model gives them (|element| below
-// 65504; beyond it the f16 operands are Inf and the outputs Inf/NaN), and each
-// element keeps an absolute precision of about 2^-25 (in the scan's bf16 form
-// the q and k rows are exact).
+// grows 2^15-fold beyond them. q and k rows enter as f16 (or hi + lo) and meet
+// in f16 planes (the P tiles): the prep records per chunk whether they lie in
+// the range those operands hold (qk_in_range: |k| < 16, |q| < 2^15, |q| |k| <
+// 256 per element, finite; L2-normalised rows lie far inside), and a
+// (sequence, v-head) with any chunk outside it runs the token-by-token f32
+// recurrence in the scan instead (the sequential form's results, NaN / Inf
+// included). Inside the range each f16 element keeps an absolute precision of
+// about 2^-25 (in the scan's bf16 form the q and k rows are exact).
 #include <type_traits>
 
 #include "xq_kernels.h"
@@ -83,9 +86,10 @@ constexpr int kColBlocks = 128 / kCols;
 // Workspace record of one (sequence, v-head, chunk), byte offsets.
 constexpr int kRecTHi = 0;                       // f16 [64][64]
 constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
-constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, max|v|[8] at 136, G[64] at 192
+constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, range flag at 129, max|v|[8] at 136, G[64] at 192
 constexpr int kRecG = 192;                      // G offset in floats within the decays
 constexpr int kRecVmax = 136;                   // largest |v| of the chunk per 16-column block (floats)
+constexpr int kRecRange = 129;                  // 1.0f when the chunk's q / k leave the operands' range, else 0
 // P tiles (bf16 rows with 16-byte loads): tile (w, jt), jt <= w, of scan wave w
 // is 1 KB at kRecP + (w (w + 1) / 2 + jt) KB; lane l's 16 bytes at 16 l are its
 // four values of P[16w + l % 16][16jt + 4(l / 16) + i] as f16 hi, then f16 lo
@@ -188,6 +192,20 @@ XQ_DEV void split3_x4(const f4& v, uint2 (&t)[3]) {
     t[2] = make_uint2(hi_halves(l[0], l[1]), hi_halves(l[2], l[3]));
 }
 
+// Whether a chunk's q and k rows lie in the range the chunked form's operands
+// hold, from the largest |element| of each (f32 bits): k below 16 and q below
+// 2^15 with |q| |k| below 256 per element pair, all finite. Then every f16
+// operand (k, q as f16 or hi + lo; K K^T, q . k <= 128 |q| |k| in the f16 P
+// tiles) stays below 2^15; L2-normalised rows (|element| <= 1) lie far
+// inside. A NaN compares false, so non-finite rows fall outside.
+XQ_DEV bool qk_in_range(uint32_t kbits, uint32_t qbits) {
+    const float km = __uint_as_float(kbits), qm = __uint_as_float(qbits);
+    return km < 16.0f && qm < 32768.0f && km * qm < 256.0f;
+}
+
+// largest |x| of the two bf16 halves of w, as f32 bits
+XQ_DEV uint32_t bf16x2_absmax_bits(uint32_t w) { return max(w & 0x7fffu, (w >> 16) & 0x7fffu) << 16; }
+
 // ---------------------------------------------------------------- prep
 
 template <bool BF16, bool VEC>
@@ -199,6 +217,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     __shared__ __attribute__((aligned(16))) float sKK[64 * FP];  // L of one v-head
     __shared__ __attribute__((aligned(16))) float sG[2][64], sBeta[2][64], sEG[2][64];
     __shared__ uint32_t sVmax[2][kColBlocks];  // bits of the largest |v| per column block
+    __shared__ uint32_t sQKmax[2];              // bits of the chunk's largest |k|, |q|
     // f32 rows: the f16 remainders of K
     constexpr int NKL = BF16 ? 8 : 64 * KP;
     __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
@@ -223,6 +242,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         const int tg = t0 + t;
         const bool ok = tg < a.T;
         const uint8_t* kr = a.k + (int64_t)b * a.k_nb3 + (int64_t)tg * a.k_nb2 + (int64_t)kh * a.k_nb1;
+        uint32_t kmx = 0, qmx = 0;  // the largest |k|, |q| of the thread's elements (f32 bits)
         if constexpr (RAW) {
             // rows past T: loads of row T - 1, zeroed (no conditional loads)
             const int tc = min(tg, a.T - 1);
@@ -240,6 +260,10 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
                 const uint4 x = wk[gi], y = wq[gi];
                 *(uint4*)(sK + t * KP + 32 * qt + 8 * gi) = make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
                 *(uint4*)(sQ + t * KP + 32 * qt + 8 * gi) = make_uint4(y.x & m, y.y & m, y.z & m, y.w & m);
+                kmx = max(kmx, max(max(bf16x2_absmax_bits(x.x), bf16x2_absmax_bits(x.y)),
+                                   max(bf16x2_absmax_bits(x.z), bf16x2_absmax_bits(x.w))) & m);
+                qmx = max(qmx, max(max(bf16x2_absmax_bits(y.x), bf16x2_absmax_bits(y.y)),
+                                   max(bf16x2_absmax_bits(y.z), bf16x2_absmax_bits(y.w))) & m);
             }
         }
 #pragma unroll
@@ -256,11 +280,25 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             const h8 hk = to_h8(xk);
             *(h8*)(sK + t * KP + i0) = hk;
             if constexpr (!BF16) *(h8*)(sKl + t * KP + i0) = lo_h8(xk, hk);
+            // q rows, read here for their range only (the scan forms P from them)
+            float xq[8];
+            if (ok) {
+                load8<BF16, VEC>(a.q + (int64_t)b * a.q_nb3 + (int64_t)tg * a.q_nb2 + (int64_t)kh * a.q_nb1, i0, xq);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xq[e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kmx = max(kmx, __float_as_uint(xk[e]) & 0x7fffffffu);
+                qmx = max(qmx, __float_as_uint(xq[e]) & 0x7fffffffu);
+            }
         }
         // largest |v| of the token's 32 columns 32qt.. (two column blocks) for
         // each v-head; a NaN compares as the largest bits, so it reaches the
         // scan's choice
         if (tid < 2 * kColBlocks) sVmax[tid / kColBlocks][tid % kColBlocks] = 0;
+        if (tid < 2) sQKmax[tid] = 0;
         uint32_t vm[2][2] = {{0, 0}, {0, 0}};
         if (ok) {
 #pragma unroll
@@ -282,6 +320,8 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             atomicMax(&sVmax[e2][2 * qt], vm[e2][0]);
             atomicMax(&sVmax[e2][2 * qt + 1], vm[e2][1]);
         }
+        atomicMax(&sQKmax[0], kmx);
+        atomicMax(&sQKmax[1], qmx);
         if (tid < 128) {
             const int e2 = tid >> 6, tt = t0 + (tid & 63), h = kh + 16 * e2;
             const bool ok2 = tt < a.T;
@@ -456,6 +496,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             dec[64 + tid] = __expf(GC - G);
             dec[kRecG + tid] = G;
             if (tid == 0) dec[128] = __expf(GC);
+            if (tid == 1) dec[kRecRange] = qk_in_range(sQKmax[0], sQKmax[1]) ? 0.0f : 1.0f;
             if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[e2][tid]);
         }
         if constexpr (RAW) {  // P[t][j] = (q_t . k_j) e^{G_t - G_j} (j <= t), f16 hi + lo
@@ -679,6 +720,52 @@ XQ_DEV void scan_load_all(const GdnChunkArgs& a, int b, int h, int cb, int n, in
     scan_load<3>(a, b, h, cb, n, wave, lr, lg, L);
 }
 
+// The token-by-token recurrence for a scan workgroup's 16 columns, in f32: the
+// chunked form's fallback for a (sequence, v-head) whose q or k rows leave
+// the range its operands hold in some chunk (qk_in_range). Lanes 16j .. 16j +
+// 15 of wave w own column 16 cb + 4w + j, lane part r its key dims 8r .. 8r +
+// 7; each token's dot products reduce over the 16 lanes.
+template <bool BF16>
+XQ_DEV void scan_sequential(const GdnChunkArgs& a, int b, int h, int cb, int wave, int lane) {
+    const int kh = h % 16, r = lane & 15, c = kCols * cb + 4 * wave + (lane >> 4);
+    const float* st = a.state + (int64_t)b * (a.s_nb3 / 4) + (int64_t)h * 16384 + (int64_t)c * 128 + 8 * r;
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = st[e];
+    float* out = a.dst + (int64_t)b * (a.dst_nb2 / 4);
+    for (int t = 0; t < a.T; ++t) {
+        float kx[8], qx[8];
+        load8<BF16, false>(a.k + (int64_t)b * a.k_nb3 + (int64_t)t * a.k_nb2 + (int64_t)kh * a.k_nb1, 8 * r, kx);
+        load8<BF16, false>(a.q + (int64_t)b * a.q_nb3 + (int64_t)t * a.q_nb2 + (int64_t)kh * a.q_nb1, 8 * r, qx);
+        const float g = *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)t * a.g_nb2 + (int64_t)h * a.g_nb1);
+        const float be = *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)t * a.b_nb2 + (int64_t)h * a.b_nb1);
+        const uint8_t* vr = a.v + (int64_t)b * a.v_nb3 + (int64_t)t * a.v_nb2 + (int64_t)h * a.v_nb1;
+        const float vv = BF16 ? bf16_bits_to_f32(((const uint16_t*)vr)[c]) : ((const float*)vr)[c];
+        const float dk = expf(g);
+        float kv = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            s[e] *= dk;
+            kv = fmaf(s[e], kx[e], kv);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) kv += __shfl_xor(kv, o);
+        const float d = (vv - kv) * be;
+        float y = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            s[e] = fmaf(kx[e], d, s[e]);
+            y = fmaf(s[e], qx[e], y);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) y += __shfl_xor(y, o);
+        if (r == 0) out[(int64_t)t * 4096 + h * 128 + c] = y * a.scale;
+    }
+    float* so = a.state_out + (int64_t)b * (a.so_nb3 / 4) + (int64_t)h * 16384 + (int64_t)c * 128 + 8 * r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) so[e] = s[e];
+}
+
 template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     constexpr int TP = 72;   // X^T, U^T rows [c][t] (halves)
@@ -726,9 +813,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 
     // ---- 2^a: the largest |S| entering the block and |v| of its columns over
     //      the prefill (the chunks' maxima from the prep) brought into [1, 2)
-    __shared__ uint32_t sAm[4];
+    //      (and whether some chunk's q / k leave the operands' range)
+    __shared__ uint32_t sAm[4], sOut[4];
     {
         uint32_t am = 0;
+        bool out_of_range = false;
 #pragma unroll
         for (int a2 = 0; a2 < 2; ++a2)
 #pragma unroll
@@ -736,7 +825,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         for (int n = lane; n < a.n_chunks; n += 64) {
             const float* dec = (const float*)(a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes + kRecDec);
             am = max(am, __float_as_uint(dec[kRecVmax + cb]) & 0x7fffffffu);
+            out_of_range |= dec[kRecRange] != 0.0f;
         }
+        const bool wave_out = __builtin_amdgcn_ballot_w64(out_of_range) != 0;  // every lane of the wave
+        if (lane == 0) sOut[wave] = wave_out ? 1u : 0u;
         am = max(am, (uint32_t)dpp_i<0xB1>((int)am));
         am = max(am, (uint32_t)dpp_i<0x4E>((int)am));
         am = max(am, (uint32_t)dpp_i<0x141>((int)am));
@@ -746,6 +838,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         if (lane == 0) sAm[wave] = am;
     }
     __syncthreads();
+    if (sOut[0] | sOut[1] | sOut[2] | sOut[3]) {  // workgroup-uniform
+        scan_sequential<BF16>(a, b, h, cb, wave, lane);
+        return;
+    }
     int pa = 0;  // the power a
     {
         const float m = __uint_as_float(max(max(sAm[0], sAm[1]), max(sAm[2], sAm[3])));

@@ -17,6 +17,7 @@
 
 // the node layout the bindings build (ctypes mirror in xqattn/__init__.py)
 static_assert(sizeof(xq_tensor) == 80, "xq_tensor layout");
+static_assert(sizeof(xq_ggml_backend_params) == 32, "xq_ggml_backend_params layout");
 static_assert(offsetof(xq_ggml_node, dst) == 72 && offsetof(xq_ggml_node, src) == 152 &&
                   sizeof(xq_ggml_node) == 232,
               "xq_ggml_node layout");
@@ -55,14 +56,17 @@ float param_f32(const xq_ggml_node* n, int i) {
 }
 
 // ggml_flash_attn_ext's op_params (scale, max_bias, logit_softcap as float
-// bits) with the backend-wide policy choices.
+// bits) with the backend-wide policy choices; the automatic split under the
+// consistent query policy is the length-only partition (batch-invariant bits).
 xq_fa_params fa_params_of(const xq_ggml_node* n, const xq_ggml_backend_params& bp) {
     xq_fa_params p{};
     p.scale = param_f32(n, 0);
     p.max_bias = param_f32(n, 1);
     p.logit_softcap = param_f32(n, 2);
     p.qk_policy = bp.fa_qk_policy;
-    p.split_mode = bp.fa_split_mode;
+    p.split_mode = bp.fa_split_mode == XQ_FA_SPLIT_AUTO && bp.fa_qk_policy == XQ_FA_QK_CONSISTENT
+                       ? XQ_FA_SPLIT_LENGTH
+                       : bp.fa_split_mode;
     p.engine = bp.fa_engine;
     return p;
 }
@@ -80,12 +84,18 @@ bool fa_supported(const xq_ggml_node* n, const xq_ggml_backend_params& bp) {
                                       &n->dst, &p) != 0;
 }
 
+// the reference's rule for min_tokens: 2 stays 2, anything else is 1
+// (d3d12_set_gdn_enabled, ggml_d3d12.cpp:68-71)
+int gdn_min_tokens_of(const xq_ggml_backend_params& bp) { return bp.gdn_min_tokens == 2 ? 2 : 1; }
+
 // d3d12_gdn_supported's operand rules (ggml_d3d12.cpp:77-109): six sources,
-// src[6..8] (the rows-indexed mode) absent, activated gates, 1..17 slots.
-bool gdn_supported(const xq_ggml_node* n) {
+// src[6..8] (the rows-indexed mode) absent, activated gates, 1..17 slots, and
+// at least the backend's minimum token count (:89).
+bool gdn_supported(const xq_ggml_node* n, const xq_ggml_backend_params& bp) {
     for (int i = 0; i < 6; ++i)
         if (!n->src[i]) return false;
     if (!srcs_absent_from(n, 6)) return false;
+    if (n->src[2]->ne[2] < gdn_min_tokens_of(bp)) return false;
     return xq_supports_gated_delta_net(n->src[0], n->src[1], n->src[2], n->src[3], n->src[4],
                                        n->src[5], &n->dst, n->op_params[0],
                                        n->op_params[1]) != 0;
@@ -96,7 +106,24 @@ bool runs_work(const xq_ggml_node* n) {
 }
 
 const xq_ggml_backend_params kDefaults = {XQ_FA_QK_CONSISTENT, XQ_FA_SPLIT_AUTO, XQ_FA_ENGINE_AUTO,
-                                          XQ_GDN_AUTO, {0, 0, 0, 0}};
+                                          XQ_GDN_AUTO, 1, {0, 0, 0}};
+
+// the one predicate the scheduler-facing supports_op and graph_compute share
+bool node_supported(const xq_ggml_node* n, const xq_ggml_backend_params& bp) {
+    switch (n->op) {
+    case XQ_GGML_OP_NOOP: return true;
+    case XQ_GGML_OP_FLASH_ATTN_EXT: return fa_supported(n, bp);
+    case XQ_GGML_OP_GATED_DELTA_NET: return gdn_supported(n, bp);
+    default: return false;
+    }
+}
+
+bool params_ok(const xq_ggml_backend_params& bp) {
+    return bp.fa_qk_policy >= XQ_FA_QK_CONSISTENT && bp.fa_qk_policy <= XQ_FA_QK_NATIVE &&
+           bp.fa_split_mode >= XQ_FA_SPLIT_AUTO && bp.fa_split_mode <= XQ_FA_SPLIT_LENGTH &&
+           bp.fa_engine >= XQ_FA_ENGINE_AUTO && bp.fa_engine <= XQ_FA_ENGINE_VALU &&
+           bp.gdn_mode >= XQ_GDN_AUTO && bp.gdn_mode <= XQ_GDN_CHUNKED;
+}
 
 struct DeviceGuard {  // restores the caller's current device
     int prev = -1;
@@ -120,11 +147,16 @@ xq_ggml_backend* xq_ggml_backend_init(int32_t device, const xq_ggml_backend_para
         err(XQ_ERR_HIP, "no HIP device %d (%d present)", device, count);
         return nullptr;
     }
-    const xq_ggml_backend_params bp = params ? *params : kDefaults;
-    if (bp.fa_qk_policy < XQ_FA_QK_CONSISTENT || bp.fa_qk_policy > XQ_FA_QK_NATIVE ||
-        bp.fa_split_mode < XQ_FA_SPLIT_AUTO || bp.fa_split_mode > XQ_FA_SPLIT_NONE ||
-        bp.fa_engine < XQ_FA_ENGINE_AUTO || bp.fa_engine > XQ_FA_ENGINE_VALU ||
-        bp.gdn_mode < XQ_GDN_AUTO || bp.gdn_mode > XQ_GDN_CHUNKED) {
+    xq_ggml_backend_params bp = params ? *params : kDefaults;
+    if (!params) {  // the defaults take the environment's ggml knobs, as ggml's op does
+        xq_fa_params fp{};
+        fp.qk_policy = bp.fa_qk_policy;
+        fp.split_mode = bp.fa_split_mode;
+        (void)xq_fa_params_from_env(&fp);
+        bp.fa_qk_policy = fp.qk_policy;
+        bp.fa_split_mode = fp.split_mode;
+    }
+    if (!params_ok(bp)) {
         err(XQ_ERR_BAD_ARG, "bad backend params");
         return nullptr;
     }
@@ -161,14 +193,11 @@ void* xq_ggml_backend_stream(const xq_ggml_backend* be) { return be ? (void*)be-
 
 size_t xq_ggml_backend_workspace_bytes(const xq_ggml_backend* be) { return be ? be->ws_bytes : 0; }
 
-int xq_ggml_supports_op(const xq_ggml_node* n) {
-    if (!n) return 0;
-    switch (n->op) {
-    case XQ_GGML_OP_NOOP: return 1;
-    case XQ_GGML_OP_FLASH_ATTN_EXT: return fa_supported(n, kDefaults) ? 1 : 0;
-    case XQ_GGML_OP_GATED_DELTA_NET: return gdn_supported(n) ? 1 : 0;
-    default: return 0;
-    }
+int xq_ggml_supports_op(const xq_ggml_node* n) { return n && node_supported(n, kDefaults) ? 1 : 0; }
+
+int xq_ggml_supports_op_params(const xq_ggml_node* n, const xq_ggml_backend_params* params) {
+    if (!n || (params && !params_ok(*params))) return 0;
+    return node_supported(n, params ? *params : kDefaults) ? 1 : 0;
 }
 
 xq_status xq_ggml_graph_compute(xq_ggml_backend* be, const xq_ggml_node* nodes, int32_t n_nodes) {
@@ -190,7 +219,7 @@ xq_status xq_ggml_graph_compute(xq_ggml_backend* be, const xq_ggml_node* nodes, 
                                                              n->src[4], &n->dst, &p, &bytes);
             if (st != XQ_OK) return st;
         } else if (n->op == XQ_GGML_OP_GATED_DELTA_NET) {
-            if (!gdn_supported(n))
+            if (!gdn_supported(n, be->params))
                 return err(XQ_ERR_UNSUPPORTED, "node %d: GATED_DELTA_NET outside the supported contract", i);
             const xq_status st = xq_gated_delta_net_workspace(n->src[0], n->src[2], n->op_params[0],
                                                               be->params.gdn_mode, &bytes);

@@ -31,7 +31,7 @@ STATUS = {0: "OK", 1: "UNSUPPORTED", 2: "BAD_SHAPE", 3: "BAD_ARG", 4: "WORKSPACE
 
 QK_CONSISTENT, QK_NATIVE = 0, 1
 SPLIT_AUTO, SPLIT_REFERENCE, SPLIT_BALANCED, SPLIT_FINE, SPLIT_COARSE, SPLIT_NONE = range(6)
-SPLIT_MQ_BALANCED, SPLIT_MQ_FINE = 6, 7
+SPLIT_MQ_BALANCED, SPLIT_MQ_FINE, SPLIT_LENGTH = 6, 7, 8
 GDN_AUTO, GDN_STEP, GDN_CHUNKED = 0, 1, 2
 ENGINE_AUTO, ENGINE_MFMA, ENGINE_VALU = 0, 1, 2
 
@@ -39,11 +39,13 @@ EXPORTS = (
     "xq_supports_flash_attn_ext", "xq_flash_attn_ext_workspace", "xq_flash_attn_ext",
     "xq_flash_attn_ext_noalloc",
     "xq_fa_range_workspace", "xq_fa_range", "xq_fa_lse_merge", "xq_fa_split_count", "xq_fa_split_rows",
+    "xq_fa_params_from_env",
     "xq_supports_gated_delta_net", "xq_gated_delta_net_workspace", "xq_gated_delta_net",
     "xq_kv_store", "xq_kv_record_bytes", "xq_last_error", "xq_abi_version",
     "xq_profile_enable", "xq_profile_reset", "xq_profile_read",
     "xq_ggml_backend_init", "xq_ggml_backend_free", "xq_ggml_backend_name", "xq_ggml_backend_stream",
-    "xq_ggml_backend_workspace_bytes", "xq_ggml_supports_op", "xq_ggml_graph_compute",
+    "xq_ggml_backend_workspace_bytes", "xq_ggml_supports_op", "xq_ggml_supports_op_params",
+    "xq_ggml_graph_compute",
 )
 
 
@@ -96,7 +98,8 @@ class XqGgmlBackendParams(ctypes.Structure):
         ("fa_split_mode", ctypes.c_int32),
         ("fa_engine", ctypes.c_int32),
         ("gdn_mode", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 4),
+        ("gdn_min_tokens", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 3),
     ]
 
 
@@ -125,6 +128,7 @@ def load() -> ctypes.CDLL:
         "xq_fa_lse_merge": (i32, [P, P, i32, i64, i32, P, P, P]),
         "xq_fa_split_count": (i32, [i64, i32]),
         "xq_fa_split_rows": (i64, [i64, i32]),
+        "xq_fa_params_from_env": (i32, [FP]),
         "xq_supports_gated_delta_net": (ctypes.c_int, [T, T, T, T, T, T, T, i32, i32]),
         "xq_gated_delta_net_workspace": (i32, [T, T, i32, i32, ctypes.POINTER(sz)]),
         "xq_gated_delta_net": (i32, [T, T, T, T, T, T, T, i32, i32, i32, P, sz, P]),
@@ -142,6 +146,7 @@ def load() -> ctypes.CDLL:
         "xq_ggml_backend_stream": (P, [P]),
         "xq_ggml_backend_workspace_bytes": (sz, [P]),
         "xq_ggml_supports_op": (ctypes.c_int, [ctypes.POINTER(XqGgmlNode)]),
+        "xq_ggml_supports_op_params": (ctypes.c_int, [ctypes.POINTER(XqGgmlNode), ctypes.POINTER(XqGgmlBackendParams)]),
         "xq_ggml_graph_compute": (i32, [P, ctypes.POINTER(XqGgmlNode), i32]),
     }
     for name, (res, args) in sig.items():
@@ -303,6 +308,13 @@ def split_count(kv_len: int, split_mode: int = SPLIT_AUTO) -> int:
     return int(load().xq_fa_split_count(kv_len, split_mode))
 
 
+def fa_params_from_env(params: XqFaParams) -> XqFaParams:
+    """Apply the environment's ggml knobs (GGML_FLASH_ATTN_NO_QUERY_TILING,
+    GGML_FLASH_ATTN_NO_SPLIT_KV) to params, as xq_fa_params_from_env does."""
+    _check(load().xq_fa_params_from_env(ctypes.byref(params)), "fa_params_from_env")
+    return params
+
+
 def split_rows(kv_len: int, split_mode: int = SPLIT_AUTO) -> int:
     return int(load().xq_fa_split_rows(kv_len, split_mode))
 
@@ -440,22 +452,35 @@ class GgmlNode:
         return n
 
 
-def ggml_supports_op(node: GgmlNode) -> bool:
-    """dev_supports_op for this backend (pure; no GPU needed)."""
+def backend_params(fa_qk_policy=QK_CONSISTENT, fa_split_mode=SPLIT_AUTO, fa_engine=ENGINE_AUTO,
+                   gdn_mode=GDN_AUTO, gdn_min_tokens=1) -> XqGgmlBackendParams:
+    p = XqGgmlBackendParams()
+    p.fa_qk_policy, p.fa_split_mode, p.fa_engine = fa_qk_policy, fa_split_mode, fa_engine
+    p.gdn_mode, p.gdn_min_tokens = gdn_mode, gdn_min_tokens
+    return p
+
+
+def ggml_supports_op(node: GgmlNode, params: XqGgmlBackendParams | None = None) -> bool:
+    """dev_supports_op for a backend with these params (None = the defaults);
+    pure, no GPU needed."""
     st = node.struct()
-    return bool(load().xq_ggml_supports_op(ctypes.byref(st)))
+    if params is None:
+        return bool(load().xq_ggml_supports_op(ctypes.byref(st)))
+    return bool(load().xq_ggml_supports_op_params(ctypes.byref(st), ctypes.byref(params)))
 
 
 class GgmlBackend:
     """The backend object: its own HIP stream, a grow-only workspace, and a
-    synchronous ``graph_compute`` over ``GgmlNode`` lists."""
+    synchronous ``graph_compute`` over ``GgmlNode`` lists. ``use_defaults``
+    passes NULL params (the defaults, with the environment's ggml
+    flash-attention knobs applied at init)."""
 
     def __init__(self, device=0, fa_qk_policy=QK_CONSISTENT, fa_split_mode=SPLIT_AUTO,
-                 fa_engine=ENGINE_AUTO, gdn_mode=GDN_AUTO):
+                 fa_engine=ENGINE_AUTO, gdn_mode=GDN_AUTO, gdn_min_tokens=1, use_defaults=False):
         lib = load()
-        p = XqGgmlBackendParams()
-        p.fa_qk_policy, p.fa_split_mode, p.fa_engine, p.gdn_mode = fa_qk_policy, fa_split_mode, fa_engine, gdn_mode
-        self._h = lib.xq_ggml_backend_init(device, ctypes.byref(p))
+        p = backend_params(fa_qk_policy, fa_split_mode, fa_engine, gdn_mode, gdn_min_tokens)
+        self.params = None if use_defaults else p
+        self._h = lib.xq_ggml_backend_init(device, None if use_defaults else ctypes.byref(p))
         if not self._h:
             raise XqError(5, "ggml_backend_init", lib.xq_last_error().decode())
 

@@ -70,23 +70,7 @@ def build(jobs: int | None = None) -> pathlib.Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
-    build_probe()
     return LIB
-
-
-PROBE_SRC = ROOT / "probe" / "stream_copy.hip"
-PROBE_LIB = PKG / "libxqprobe.so"
-
-
-def build_probe() -> pathlib.Path:
-    """The benchmark's HBM copy probe (libxqprobe.so), apart from the library."""
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *CFLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{r.stderr}")
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
 
 
 if __name__ == "__main__":
