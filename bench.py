@@ -192,8 +192,9 @@ def quantile(sorted_vals, f):
 
 
 def dist_ms(sorted_ms):
-    """median / p10 / p90 in microseconds of ascending millisecond samples."""
-    return {"median_us": round(1000 * quantile(sorted_ms, 0.5), 3), "p10_us": round(1000 * quantile(sorted_ms, 0.1), 3),
+    """mean / median / p10 / p90 in microseconds of ascending millisecond samples."""
+    return {"mean_us": round(1000 * statistics.fmean(sorted_ms), 3),
+            "median_us": round(1000 * quantile(sorted_ms, 0.5), 3), "p10_us": round(1000 * quantile(sorted_ms, 0.1), 3),
             "p90_us": round(1000 * quantile(sorted_ms, 0.9), 3), "samples": len(sorted_ms)}
 
 
@@ -271,7 +272,10 @@ def summarize_pmc(fetch_dir, write_dir, kernel, workload, copy_bytes, command):
     out = {}
     for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         vals = per_dispatch(d, counter)
-        kern = [v for k, v in vals.items() if kernel in k]
+        # the workload's own launches (the --only fa run also times the other
+        # attention legs, whose fa_dec instantiations differ)
+        sig = {"fa_dec": "fa_dec<8, 256, 1,", "gdn_step": "gdn_step_kernel"}.get(kernel, kernel)
+        kern = [v for k, v in vals.items() if sig in k]
         copies = vals.get("copy", {})
         if not kern or not copies:
             raise SystemExit(f"{counter}: kernel {kernel!r} or the calibration copy not found in {d}")
@@ -330,13 +334,102 @@ def copy_ceiling(torch, total_bytes, n_sets, steps, warmup, read_only):
         res = torch.empty((), dtype=torch.float32, device="cuda")
 
         def read_call(i):
-            torch.sum(whole[i], out=res)
+            torch.sum(whole[i], dim=0, out=res)
 
         r_ms = time_calls(torch, read_call, n_sets, steps, warmup)
         ceil["read_sum"] = {"us_per_call": round(r_ms * 1000, 3), "GB/s": round(2 * half / (r_ms * 1e-3) / 1e9, 1)}
         log(f"read ceiling (sum): {r_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
         del whole
     return ceil
+
+
+# Which bench leg a traced dispatch belongs to: its kernel's template signature
+# (fa_reduce takes the leg of the fa_dec launch right before it; the two
+# prefills differ in their scan grid: 256 workgroups for one sequence).
+TRACE_LEGS = (
+    ("fa_dec<8, 256, 1,", "fa_decode_q8_0_h24kv4_d256_L32768_b4"),
+    ("fa_dec<1, 128, 1,", "fa_decode_f16_h16kv8_d128_L4096"),
+    ("fa_dec<2, 128, 2,", "fa_verify_q4_0_nq8_h32kv8_d128_L16392_b8"),
+    ("gdn_step_kernel", "gdn_step_hk16_hv32_d128_b8"),
+    ("gdn_chunk_", "gdn_prefill_T4096_c64_bf16"),
+)
+
+
+def _stats_us(vals):
+    v = sorted(vals)
+    return {"launches": len(v), "mean_us": round(statistics.fmean(v), 3), "median_us": round(quantile(v, 0.5), 3),
+            "p10_us": round(quantile(v, 0.1), 3), "p90_us": round(quantile(v, 0.9), 3),
+            "min_us": round(v[0], 3), "max_us": round(v[-1], 3)}
+
+
+def summarize_trace(trace_dir, command, back_to_back_gap_us=2.0):
+    """Per-leg kernel statistics from a rocprofv3 --kernel-trace CSV of a bench
+    run: every dispatch's device duration (end - start), split into launches
+    that start within back_to_back_gap_us of the previous dispatch's end (the
+    graph replays and eager passes queued back to back) and launches that
+    start after an idle GPU (the one-call-at-a-time event pass).
+    Returns {leg: markdown text}."""
+    import csv
+    import glob
+    rows = []
+    for path in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(path)):
+            grid = (int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0) * int(r.get("Grid_Size_Y") or 1)
+                    * int(r.get("Grid_Size_Z") or 1))  # threads in the whole grid
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"], grid))
+    if not rows:
+        raise SystemExit(f"no kernel trace CSV under {trace_dir}")
+    rows.sort()
+    legs = {}
+    prev_end, last_fa_leg = None, None
+    for start, end, name, grid in rows:
+        leg = None
+        for sig, wl_name in TRACE_LEGS:
+            if sig in name:
+                leg = wl_name
+        if "fa_reduce" in name:
+            leg = last_fa_leg
+        if "fa_dec<" in name:
+            last_fa_leg = leg
+        if leg == "gdn_prefill_T4096_c64_bf16" and "gdn_chunk_scan" in name and grid > 256 * 256:
+            leg = "gdn_prefill_T4096_c64_bf16_b8"
+        if leg == "gdn_prefill_T4096_c64_bf16" and "gdn_chunk_prep" in name and grid > 64 * 16 * 256:
+            leg = "gdn_prefill_T4096_c64_bf16_b8"
+        gap = None if prev_end is None else (start - prev_end) / 1000.0
+        prev_end = end if prev_end is None else max(prev_end, end)
+        if leg is None:
+            continue
+        kname = name.split("(")[0].replace("void ", "")
+        d = legs.setdefault(leg, {}).setdefault(kname, {"all": [], "b2b": [], "alone": []})
+        us = (end - start) / 1000.0
+        d["all"].append(us)
+        (d["b2b"] if gap is not None and gap < back_to_back_gap_us else d["alone"]).append(us)
+    out = {}
+    for leg, kernels in legs.items():
+        lines = [f"# Kernel trace of {leg}", "",
+                 "Command (run from /tmp; $R = the repository root):", ""]
+        lines += [f"    {c}" for c in command]
+        lines += ["", f"Device durations (end - start) of every traced dispatch of this leg, in microseconds,",
+                  f"from rocprofv3's kernel trace CSV, summarized by `bench.py --summarize-trace`. "
+                  f"`back to back`: the dispatch started within {back_to_back_gap_us} us of the previous "
+                  f"dispatch's end (graph replays, eager passes queued ahead); `after idle`: the GPU was idle "
+                  f"before it (the bench's one-call-at-a-time event pass).", "",
+                  "| kernel | dispatches | launches | mean | median | p10 | p90 | min | max |",
+                  "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+        rec = {"workload": leg, "kernels": {}}
+        for kname, d in kernels.items():
+            rec["kernels"][kname] = {}
+            for part in ("all", "b2b", "alone"):
+                if not d[part]:
+                    continue
+                st = _stats_us(d[part])
+                rec["kernels"][kname][part] = st
+                label = {"all": "all", "b2b": "back to back", "alone": "after idle"}[part]
+                lines.append(f"| `{kname}` | {label} | {st['launches']} | {st['mean_us']} | {st['median_us']} | "
+                             f"{st['p10_us']} | {st['p90_us']} | {st['min_us']} | {st['max_us']} |")
+        lines += ["", json.dumps(rec)]
+        out[leg] = "\n".join(lines) + "\n"
+    return out
 
 
 def kernel_times(torch, xq, fn, n_sets, steps):
@@ -415,7 +508,20 @@ def main():
     ap.add_argument("--pmc-kernel", choices=["fa_dec", "gdn_step"], default="fa_dec",
                     help="kernel of the --summarize-pmc summary (fa_dec: 32k q8_0 decode; gdn_step: 8-sequence step)")
     ap.add_argument("--pmc-command", action="append", default=[], help="command lines recorded in the summary")
+    ap.add_argument("--summarize-trace", metavar="TRACE_DIR",
+                    help="write profiles/<kernel>_<workload>_kernel_trace.md for every leg found in a rocprofv3 "
+                         "--kernel-trace output dir of a bench run (--pmc-command gives the command lines) and exit")
     args = ap.parse_args()
+    if args.summarize_trace:
+        kern_of = {"fa_decode_q8_0_h24kv4_d256_L32768_b4": "fa_dec", "fa_decode_f16_h16kv8_d128_L4096": "fa_dec",
+                   "fa_verify_q4_0_nq8_h32kv8_d128_L16392_b8": "fa_dec", "gdn_step_hk16_hv32_d128_b8": "gdn_step",
+                   "gdn_prefill_T4096_c64_bf16": "gdn_chunk", "gdn_prefill_T4096_c64_bf16_b8": "gdn_chunk"}
+        for leg, text in summarize_trace(args.summarize_trace, args.pmc_command).items():
+            path = ROOT / "profiles" / f"{kern_of.get(leg, 'kernels')}_{leg}_kernel_trace.md"
+            path.parent.mkdir(exist_ok=True)
+            path.write_text(text)
+            print(path)
+        return
     if args.summarize_pmc:
         from xqattn import workloads as wl
         workload = {"fa_dec": wl.FA_C2.name, "gdn_step": wl.GDN_C3.name}[args.pmc_kernel]

@@ -32,10 +32,10 @@
 //           the B operand, so the softmax weights never leave registers and
 //           every per-pair quantity (maximum, sum, rescale factor) is
 //           lane-local.
-//           q8_0 / q4_0 V: v_mfma_f32_16x16x32_f16 on the exact integer values
+//           q8_0 / q4_0 V: v_mfma_f32_16x16x16_f16 on the exact integer values
 //           as f16 (q4_0's high nibbles as 16x theirs, undone exactly at the
-//           merge), the four rows repeated, against w * 2^S_p * d_v as f16
-//           high + low parts: each product formed in f32 by v_fma_mix, its f16
+//           merge), once against the high and once against the low parts of
+//           w * 2^S_p * d_v as f16: each product formed in f32 by v_fma_mix, its f16
 //           rounding h and the remainder w * 2^S_p * d_v - h as f16, about 22
 //           significant bits (ggml multiplies the weight by the f32 dequantized
 //           value, one f32 rounding). 2^S_p, a power of two per pair sized from
@@ -44,11 +44,11 @@
 //           subnormals, and then to zero, as V's magnitude shrinks); it enters
 //           the weights' exponent argument and leaves at the merge, both
 //           exactly.
-//           F16 / E5M2 V: v_mfma_f32_16x16x32_f16 on the exact f16 V against
-//           the weight as f16 high + low parts (products 8lg..8lg+3 of a lane
-//           group: its four rows' high parts, 8lg+4..8lg+7: their low parts;
-//           the V operand repeats the four rows), about 22 significant bits of
-//           every weight (the weights lie in (0, 16]).
+//           F16 / E5M2 V: v_mfma_f32_16x16x16_f16 on the exact f16 V, once
+//           against the weights' f16 high parts and once against their low
+//           parts, about 22 significant bits of every weight (the weights lie
+//           in (0, 16]). Two 16x16x16 products read the same V registers; one
+//           16x16x32 product would need the rows repeated (two moves per tile).
 // Online softmax in base 2 (scores pre-multiplied by log2 e) with a lazy
 // maximum: the running maximum moves only when a slice exceeds it by more
 // than 8, so accumulator rescales are rare; weights are taken relative to the
@@ -151,10 +151,12 @@ XQ_DEV int64_t k_block_bytes(const uint8_t* rec, int b, int g) {
 // V^T operands of one q8_0 block: the signed bytes 0 (tile 0) and 1 (tile 1)
 // of the rows' 16-bit words x0..x3 as f16 pairs (rows 0,1 and rows 2,3),
 // exact. Each pair is two SDWA conversions of sign-extended bytes, the second
-// writing the high half and keeping the low one. The trailing s_nop gives the
+// writing the high half and keeping the low one. The words are 16-bit asm
+// operands: the conversions read their low bytes only, so the registers' high
+// halves need no clearing after the LDS loads. The trailing s_nop gives the
 // two wait states an MFMA reading a VGPR needs after a VALU wrote it (the
 // compiler's hazard tracking does not see into the asm).
-XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32_t (&A0)[2], uint32_t (&A1)[2]) {
+XQ_DEV void q8_vt_f16(uint16_t x0, uint16_t x1, uint16_t x2, uint16_t x3, uint32_t (&A0)[2], uint32_t (&A1)[2]) {
     asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
         "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
         "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
@@ -166,6 +168,14 @@ XQ_DEV void q8_vt_f16(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3, uint32
         "s_nop 1"
         : "=&v"(A0[0]), "=&v"(A0[1]), "=&v"(A1[0]), "=&v"(A1[1])
         : "v"(x0), "v"(x1), "v"(x2), "v"(x3));
+}
+
+// Bytes b0, b1 (16-bit asm operands, high halves unread) as the 16-bit halves of
+// one word, zero-extended: one v_perm and no clearing of the loads' high bits.
+XQ_DEV uint32_t pack_bytes(uint16_t b0, uint16_t b1) {
+    uint32_t r;
+    asm("v_perm_b32 %0, %1, %2, %3" : "=v"(r) : "v"(b1), "v"(b0), "s"(0x0c040c00u));
+    return r;
 }
 
 // B operand of a quantized-V value product: the f32 weights w0..w3 (rows 0..3)
@@ -224,6 +234,17 @@ XQ_DEV uint32_t f16x2_nonfinite(uint32_t w) { return ((w & 0x7c007c00u) + 0x0400
 XQ_DEV uint32_t f16x2_finite_mask(uint32_t w) { return ~((f16x2_nonfinite(w) >> 15) * 0xffffu); }
 // Nonzero when any E5M2 byte of w is Inf or NaN.
 XQ_DEV uint32_t e5m2x4_nonfinite(uint32_t w) { return ((w & 0x7c7c7c7cu) + 0x04040404u) & 0x80808080u; }
+
+// The largest of four scores in two instructions (v_max3 then v_max; a quiet
+// NaN operand is ignored, as fmaxf does, and the scores are never signalling
+// NaNs, so the canonicalising moves the compiler adds around fmaxf are not
+// needed).
+XQ_DEV float max4(float a, float b, float c, float d) {
+    float t, r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(t) : "v"(a), "v"(b), "v"(c));
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(t), "v"(d));
+    return r;
+}
 
 // Reductions over the four 16-lane rows (lanes l, l^16, l^32, l^48) by
 // permlane swaps; every lane gets the same bits ((r0 op r2) op (r1 op r3)).
@@ -584,7 +605,9 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 qb[m][c] = KT == XQ_TYPE_Q4_0
                                ? (int64_t)(((uint64_t)lds_u32(img + 32 * c + 16 + 4 * lg) << 32) | lds_u32(img + 32 * c + 4 * lg))
                                : *(const int64_t*)(img + 32 * c + 8 * lg);
-                if (c % 4 == 0) dqb[m][c / 4] = ((const float*)(img + D))[c + lg];
+                // without softcap the score scale (times log2 e) rides on d_q: the
+                // block products then give the base-2 scores directly
+                if (c % 4 == 0) dqb[m][c / 4] = ((const float*)(img + D))[c + lg] * (SOFTCAP ? 1.0f : a.scale * kLog2e);
             }
         }
     }
@@ -671,9 +694,8 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     };
 
     // ---- values of the slice in ring stage ST, block c:
-    //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x W^T, the 32
-    //      products of a lane group being its four rows' weight high parts, then
-    //      their low parts (the V operand repeats the four rows)
+    //      acc[m][2c + t] += V^T(rows 4lg..4lg+3, tile dims) x W^T, as two
+    //      products: the weights' high parts, then their low parts
     //      pw: f32 weights (row 4lg + i, pair 16m + lr; quantized V: times
     //      2^S_p); seenm: careful slice's masks of the rows the pair sees;
     //      Bf: F16/E5M2 weight operands; vsan: F16/E5M2: Inf/NaN V elements
@@ -685,22 +707,20 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         constexpr bool careful = decltype(careful_tag)::value;  // a separate copy: no mask selects when false
         const uint8_t* Vs = ring + ST * 2 * SLICE + SLICE;
         uint32_t X[4];
+        uint16_t X16[4];  // q8_0: the rows' 16-bit words (16-bit asm operands)
         if constexpr (KT == XQ_TYPE_Q4_0) {
             // byte lr of rows (0,1) and (2,3) as the halves of X[0], X[1]
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const uint8_t* vr = Vs + (4 * lg + 2 * e) * REC + 18 * c + 2 + lr;
-                u16x2 p;
-                p.x = vr[0];
-                p.y = vr[REC];
-                X[e] = __builtin_bit_cast(uint32_t, p);
+                X[e] = pack_bytes(vr[0], vr[REC]);
             }
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint8_t* vr = Vs + (4 * lg + e) * REC;
                 if constexpr (KT == XQ_TYPE_Q8_0)
-                    X[e] = lds_u16(vr + 34 * c + 2 + 2 * lr);
+                    X16[e] = *(const uint16_t*)(vr + 34 * c + 2 + 2 * lr);
                 else if constexpr (KT == XQ_TYPE_F16)
                     X[e] = lds_u32(vr + 2 * (32 * c + 2 * lr));
                 else
@@ -708,15 +728,14 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             }
         }
         if constexpr (QUANT) {
-            // B: w * 2^S * d_v as f16 high + low parts (products 8lg..8lg+3 of a
-            // lane group: rows 0..3's high parts, 8lg+4..8lg+7: their low parts);
-            // the pair's power of two 2^S keeps every high part in f16's normal
-            // range
+            // B: w * 2^S * d_v as f16 high parts (Bh) and low parts (Bl) of rows
+            // (0,1), (2,3); the pair's power of two 2^S keeps every high part in
+            // f16's normal range
             uint32_t dvw[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) dvw[i] = lds_u32(Vs + (4 * lg + i) * REC + ((BB * c) & ~3));
             const bool dhi = ((BB * c) & 2) != 0;  // the scale sits in the high half of its dword
-            h8 Bv[MT];
+            h4 Bh[MT], Bl[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
                 uint32_t b01, b23, l01, l23;
@@ -724,24 +743,26 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     wd_f16x2<true>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23, l01, l23);
                 else
                     wd_f16x2<false>(pw[m][0], pw[m][1], pw[m][2], pw[m][3], dvw[0], dvw[1], dvw[2], dvw[3], b01, b23, l01, l23);
-                if (vsan) {
-                    // an Inf/NaN scale: the low part of its product (Inf - Inf)
-                    // is set to 0, so the high part alone gives q * d's Inf / NaN
-                    l01 &= f16x2_finite_mask(b01);
-                    l23 &= f16x2_finite_mask(b23);
-                }
-                if constexpr (careful) {  // rows the pair does not see add 0, whatever their scale holds
+                if constexpr (careful) {
+                    if (vsan) {
+                        // an Inf/NaN scale: the low part of its product (Inf - Inf)
+                        // is set to 0, so the high part alone gives q * d's Inf / NaN
+                        l01 &= f16x2_finite_mask(b01);
+                        l23 &= f16x2_finite_mask(b23);
+                    }
+                    // rows the pair does not see add 0, whatever their scale holds
                     b01 &= seenm[m][0];
                     b23 &= seenm[m][1];
                     l01 &= seenm[m][0];
                     l23 &= seenm[m][1];
                 }
-                Bv[m] = __builtin_bit_cast(h8, uint4{b01, b23, l01, l23});
+                Bh[m] = __builtin_bit_cast(h4, uint2{b01, b23});
+                Bl[m] = __builtin_bit_cast(h4, uint2{l01, l23});
             }
             // A: the integer values of tile t's dims in rows (0,1), (2,3) as f16 (exact)
             uint32_t A0[2], A1[2];
             if constexpr (KT == XQ_TYPE_Q8_0) {
-                q8_vt_f16(X[0], X[1], X[2], X[3], A0, A1);
+                q8_vt_f16(X16[0], X16[1], X16[2], X16[3], A0, A1);
             } else {
                 // q4_0: the low nibble n (dim lr of the block) as 1024 + n - 1032 =
                 // n - 8, the high nibble (dim 16 + lr) unshifted as 1024 + 16n - 1152
@@ -756,13 +777,20 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     A1[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, hi) + h2{(_Float16)-1152.0f, (_Float16)-1152.0f});
                 }
             }
-            // the four rows repeated: once against the high parts, once against the low
-            const h8 At0 = __builtin_bit_cast(h8, uint4{A0[0], A0[1], A0[0], A0[1]});
-            const h8 At1 = __builtin_bit_cast(h8, uint4{A1[0], A1[1], A1[0], A1[1]});
+            // the four rows against the high parts, then against the low parts: two
+            // 16x16x16 products read the same V registers (one 16x16x32 product
+            // would need the rows repeated in four registers, two moves per tile)
+            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
+            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At0, Bv[m], acc[m][2 * c], 0, 0, 0);
-                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At1, Bv[m], acc[m][2 * c + 1], 0, 0, 0);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bh[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bh[m], acc[m][2 * c + 1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, Bl[m], acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, Bl[m], acc[m][2 * c + 1], 0, 0, 0);
             }
         } else {
             // A: f16 pairs of rows (0,1), (2,3) of tiles t = 0, 1 (exact)
@@ -782,12 +810,19 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                     A1[e] = f16x2_zero_nonfinite(A1[e]);
                 }
             }
-            const h8 At0 = __builtin_bit_cast(h8, uint4{A0[0], A0[1], A0[0], A0[1]});
-            const h8 At1 = __builtin_bit_cast(h8, uint4{A1[0], A1[1], A1[0], A1[1]});
+            const h4 At0 = __builtin_bit_cast(h4, uint2{A0[0], A0[1]});
+            const h4 At1 = __builtin_bit_cast(h4, uint2{A1[0], A1[1]});
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At0, Bf[m], acc[m][2 * c], 0, 0, 0);
-                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(At1, Bf[m], acc[m][2 * c + 1], 0, 0, 0);
+                const h4 bh = __builtin_shufflevector(Bf[m], Bf[m], 0, 1, 2, 3);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, bh, acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, bh, acc[m][2 * c + 1], 0, 0, 0);
+            }
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const h4 bl = __builtin_shufflevector(Bf[m], Bf[m], 4, 5, 6, 7);
+                acc[m][2 * c] = __builtin_amdgcn_mfma_f32_16x16x16f16(At0, bl, acc[m][2 * c], 0, 0, 0);
+                acc[m][2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(At1, bl, acc[m][2 * c + 1], 0, 0, 0);
             }
         }
     };
@@ -862,6 +897,46 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
+        // -- F16/E5M2 V: a non-finite element must reach exactly its own dim of
+        //    the pairs that see its row, as ggml's per-dim accumulation does
+        //    (VKQ += v * vs). It must not reach the pairs that do not see the
+        //    row through the shared V operand, and Inf times a weight's low
+        //    part could give NaN where the product is Inf. Lane (lr, lg) scans
+        //    its sixteenth of rows 4lg..4lg+3 here (0 * x is +-0 for finite x,
+        //    NaN otherwise), the reads overlapping the softmax; when any element
+        //    is Inf/NaN the V operands are sanitised and the bad elements are
+        //    added after the products (vrb: bit i = row 4lg + i holds one)
+        uint32_t vrb = 0;
+        if constexpr (!QUANT) {
+            constexpr int ES = KT == XQ_TYPE_F16 ? 2 : 1;
+            constexpr int SPAN = ES * D / 16;  // bytes per lane per row (8..32)
+            const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint8_t* vr = Vs + (4 * lg + i) * REC + lr * SPAN;
+                uint32_t bad = 0;
+                if constexpr (KT == XQ_TYPE_F16) {
+                    h2 z = h2{(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+                    for (int k = 0; k < SPAN / 16; ++k) {
+                        const uint4 w = *(const uint4*)(vr + 16 * k);
+                        const h2 zero = h2{(_Float16)0.0f, (_Float16)0.0f};
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.x), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.y), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.z), zero, z);
+                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.w), zero, z);
+                    }
+                    bad = __builtin_bit_cast(uint32_t, z) & 0x7fff7fffu;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < SPAN / 8; ++k) {
+                        const uint2 w = *(const uint2*)(vr + 8 * k);
+                        bad |= e5m2x4_nonfinite(w.x) | e5m2x4_nonfinite(w.y);
+                    }
+                }
+                vrb |= bad ? 1u << i : 0u;
+            }
+        }
         // quantized V: lane l reads the block scales of row l/4 (largest exponent
         // field er), used after the softmax
         // (dsan: some block scale of the slice is Inf/NaN)
@@ -888,16 +963,17 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const h2 mh = __builtin_bit_cast(h2, mw[m][i >> 1]);
-                const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : s[m][i] * sc2;
+                const float v = SOFTCAP ? cap2 * tanhf(s[m][i] * a.scale) : QUANT ? s[m][i] : s[m][i] * sc2;
                 x[m][i] = fmaf(slope2[m], (float)mh[i & 1], v);
             }
             // a sum of finite scores (|x| far below the f32 range) is finite
             // exactly when every score is: one test for -inf, +inf and NaN
             nonfin |= !__builtin_isfinite((x[m][0] + x[m][1]) + (x[m][2] + x[m][3]));
         }
-        // careful slice: rows past a pair's limit, masked rows or non-finite
-        // scores; unseen rows (past the limit, mask -inf) become -inf
-        const bool careful = t + kSub > r_all || __builtin_amdgcn_ballot_w64(nonfin) != 0;
+        // careful slice: rows past a pair's limit, masked rows, non-finite
+        // scores or (quantized V) a non-finite block scale; unseen rows (past
+        // the limit, mask -inf) become -inf
+        const bool careful = t + kSub > r_all || __builtin_amdgcn_ballot_w64(nonfin) != 0 || dsan;
         if (careful) {
 #pragma unroll
             for (int m = 0; m < MT; ++m)
@@ -916,7 +992,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         bool over = false;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            lmax[m] = fmaxf(fmaxf(x[m][0], x[m][1]), fmaxf(x[m][2], x[m][3]));
+            lmax[m] = max4(x[m][0], x[m][1], x[m][2], x[m][3]);
             over |= lmax[m] > m_run[m] + kLazyMax;
         }
         if (__builtin_amdgcn_ballot_w64(over)) {
@@ -1021,48 +1097,14 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 }
             }
         }
-        // -- F16/E5M2 V: a non-finite element must reach exactly its own dim of
-        //    the pairs that see its row, as ggml's per-dim accumulation does
-        //    (VKQ += v * vs). It must not reach the pairs that do not see the
-        //    row through the shared V operand, and Inf times a weight's low
-        //    part could give NaN where the product is Inf. Lane (lr, lg) scans
-        //    its sixteenth of rows 4lg..4lg+3 (0 * x is +-0 for finite x, NaN
-        //    otherwise); when any element is Inf/NaN the V operands are
-        //    sanitised and the bad elements are added after the products
+        // -- F16/E5M2 V: whether a row of the slice holds an Inf/NaN element (the
+        //    scan above), and which
         bool vsan = false;
         uint32_t rowbad = 0;  // rows of the slice holding a non-finite V element (vsan only)
         if constexpr (!QUANT) {
-            constexpr int ES = KT == XQ_TYPE_F16 ? 2 : 1;
-            constexpr int SPAN = ES * D / 16;  // bytes per lane per row (8..32)
-            const uint8_t* Vs = ring + S * 2 * SLICE + SLICE;
-            uint32_t rb = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint8_t* vr = Vs + (4 * lg + i) * REC + lr * SPAN;
-                uint32_t bad = 0;
-                if constexpr (KT == XQ_TYPE_F16) {
-                    h2 z = h2{(_Float16)0.0f, (_Float16)0.0f};
-#pragma unroll
-                    for (int k = 0; k < SPAN / 16; ++k) {
-                        const uint4 w = *(const uint4*)(vr + 16 * k);
-                        const h2 zero = h2{(_Float16)0.0f, (_Float16)0.0f};
-                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.x), zero, z);
-                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.y), zero, z);
-                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.z), zero, z);
-                        z = __builtin_elementwise_fma(__builtin_bit_cast(h2, w.w), zero, z);
-                    }
-                    bad = __builtin_bit_cast(uint32_t, z) & 0x7fff7fffu;
-                } else {
-#pragma unroll
-                    for (int k = 0; k < SPAN / 8; ++k) {
-                        const uint2 w = *(const uint2*)(vr + 8 * k);
-                        bad |= e5m2x4_nonfinite(w.x) | e5m2x4_nonfinite(w.y);
-                    }
-                }
-                rb |= bad ? 1u << i : 0u;
-            }
-            vsan = __builtin_amdgcn_ballot_w64(rb != 0) != 0;
+            vsan = __builtin_amdgcn_ballot_w64(vrb != 0) != 0;
             if (vsan) {
+                uint32_t rb = vrb;
                 rb |= (uint32_t)dpp_i<0xB1>((int)rb);
                 rb |= (uint32_t)dpp_i<0x4E>((int)rb);
                 rb |= (uint32_t)dpp_i<0x141>((int)rb);

@@ -203,8 +203,25 @@ XQ_DEV bool qk_in_range(uint32_t kbits, uint32_t qbits) {
     return km < 16.0f && qm < 32768.0f && km * qm < 256.0f;
 }
 
-// largest |x| of the two bf16 halves of w, as f32 bits
-XQ_DEV uint32_t bf16x2_absmax_bits(uint32_t w) { return max(w & 0x7fffu, (w >> 16) & 0x7fffu) << 16; }
+// Running maximum of |x| over bf16 pairs: m holds two 16-bit magnitude fields
+// (the bf16 bits without sign), updated by one packed unsigned maximum
+XQ_DEV uint32_t bf16x2_absmax(uint32_t m, uint32_t w) {
+    typedef unsigned short u16x2v __attribute__((ext_vector_type(2)));
+    const u16x2v a = __builtin_bit_cast(u16x2v, m), b = __builtin_bit_cast(u16x2v, w & 0x7fff7fffu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+// f32 bits of the larger magnitude field of bf16x2_absmax's result
+XQ_DEV uint32_t bf16x2_max_bits(uint32_t m) { return max(m & 0xffffu, m >> 16) << 16; }
+
+// the largest of v over the wave (unsigned)
+XQ_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x140>((int)v));  // the 16-lane row's maximum in every lane
+    v = max(v, (uint32_t)__shfl_xor((int)v, 16));
+    return max(v, (uint32_t)__shfl_xor((int)v, 32));
+}
 
 // ---------------------------------------------------------------- prep
 
@@ -260,11 +277,11 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
                 const uint4 x = wk[gi], y = wq[gi];
                 *(uint4*)(sK + t * KP + 32 * qt + 8 * gi) = make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
                 *(uint4*)(sQ + t * KP + 32 * qt + 8 * gi) = make_uint4(y.x & m, y.y & m, y.z & m, y.w & m);
-                kmx = max(kmx, max(max(bf16x2_absmax_bits(x.x), bf16x2_absmax_bits(x.y)),
-                                   max(bf16x2_absmax_bits(x.z), bf16x2_absmax_bits(x.w))) & m);
-                qmx = max(qmx, max(max(bf16x2_absmax_bits(y.x), bf16x2_absmax_bits(y.y)),
-                                   max(bf16x2_absmax_bits(y.z), bf16x2_absmax_bits(y.w))) & m);
+                kmx = bf16x2_absmax(bf16x2_absmax(bf16x2_absmax(bf16x2_absmax(kmx, x.x & m), x.y & m), x.z & m), x.w & m);
+                qmx = bf16x2_absmax(bf16x2_absmax(bf16x2_absmax(bf16x2_absmax(qmx, y.x & m), y.y & m), y.z & m), y.w & m);
             }
+            kmx = bf16x2_max_bits(kmx);
+            qmx = bf16x2_max_bits(qmx);
         }
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) {
@@ -320,8 +337,12 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             atomicMax(&sVmax[e2][2 * qt], vm[e2][0]);
             atomicMax(&sVmax[e2][2 * qt + 1], vm[e2][1]);
         }
-        atomicMax(&sQKmax[0], kmx);
-        atomicMax(&sQKmax[1], qmx);
+        kmx = wave_max_u32(kmx);
+        qmx = wave_max_u32(qmx);
+        if (lane == 0) {
+            atomicMax(&sQKmax[0], kmx);
+            atomicMax(&sQKmax[1], qmx);
+        }
         if (tid < 128) {
             const int e2 = tid >> 6, tt = t0 + (tid & 63), h = kh + 16 * e2;
             const bool ok2 = tt < a.T;
