@@ -39,11 +39,12 @@ def test_fa_config_parity(torch_gpu, cfg, engine):
     ref64, lse64 = oracle_f64(case)
     err64 = assert_close(got, ref64, what=f"{cfg.name} vs float64 closed form")
     assert_close(glse, lse64, atol=1e-4, rtol=1e-5, what=f"{cfg.name} LSE")
-    print(f"{cfg.name} engine {engine}: max|gpu-ggml|={err:.2e} max|gpu-f64|={err64:.2e}")
     # f32 accumulation on both engines; the matrix-core engine's value
     # operands (weight, or weight x block scale) carry about 22 significant
     # bits as f16 hi + lo
     rel64 = err64 / float(np.abs(ref64).max())
+    print(f"{cfg.name} engine {engine}: max|gpu-ggml|={err:.2e} max|gpu-f64|={err64:.2e} "
+          f"(/ max|f64| {rel64:.2e})")
     assert rel64 < 1e-5, rel64
 
 

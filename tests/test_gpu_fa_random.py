@@ -76,4 +76,4 @@ def test_fa_random_shapes(torch_gpu, i):
     # f32, as ggml's f32 products w * (q * d) do
     scale = max(float(np.abs(ref64).max()), 1e-30)
     assert err64 / scale < 1e-5, (note, err64 / scale)
-    print(f"{note}: max|gpu-f64| {err64:.2e}")
+    print(f"{note}: max|gpu-f64| {err64:.2e}, / max|f64| {err64 / scale:.2e}")

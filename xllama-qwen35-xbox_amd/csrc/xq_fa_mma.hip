@@ -289,11 +289,6 @@ XQ_DEV void lds_dma(const uint8_t* base, uint32_t off, uint8_t* lds) {
         asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m0)
                      : "memory", "m0");
 }
-// Same with a per-lane 64-bit address (4 bytes per lane).
-XQ_DEV void lds_dma4_ptr(const void* g, uint8_t* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
-}
 
 // Head dim held by accumulator register i of value tile (block c, half t) in
 // lane group lg. q8_0 / F16 / E5M2 tiles take dims 32c + 2n + t (n = tile
@@ -382,13 +377,16 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         } else {
             // rows from tr = min(t0, r_end - 1); lane rows clamp to r_end - 1, so
             // every offset is non-negative and below 16 rows (the whole slice
-            // may lie past the end)
+            // may lie past the end). The lane's row relative to tr is formed
+            // from its fixed slice row and two wave-uniform terms, so no
+            // per-lane row index is carried through the loop for this branch.
             const int tr = min(t0, r_end - 1);
+            const int d0 = t0 - tr, last = r_end - 1 - tr;
             const uint8_t* bt = base + (int64_t)tr * nb1;
 #pragma unroll
             for (int i = 0; i < NIS; ++i) {
-                const int row = min(t0 + crow[i], r_end - 1);
-                const uint32_t o = off[i] + (uint32_t)(row - tr - crow[i]) * (uint32_t)nb1;
+                const int rel = min(crow[i] + d0, last);  // row - tr
+                const uint32_t o = off[i] + (uint32_t)(rel - crow[i]) * (uint32_t)nb1;
                 if (CPS % 64 == 0 || i + 1 < NIS || lane < CPS % 64) lds_dma<CS, MT == 1 && REC % 128 == 0>(bt, o, dst + i * 64 * CS);
             }
         }
@@ -397,7 +395,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // ---- per-pair state of this lane's pairs 16m + lr (identical in the four lane groups)
     float m_run[MT], l_run[MT], slope2[MT];
     int lim[MT];
-    const uint16_t* mrow[MT];
+    uint32_t moff[MT];  // mask: the lane's offset in the sequence's plane (row, head, element 4lg)
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         m_run[m] = -INFINITY;
@@ -416,9 +414,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         }
         // padding pairs read the first pair's mask row (always valid memory); with
         // no mask every pair reads the first f16 pair of a zero row
-        mrow[m] = a.mask ? (const uint16_t*)(a.mask + (int64_t)(iq0 + qq) * a.m_nb1 + (int64_t)(h % a.m_ne2) * a.m_nb2 +
-                                             (int64_t)(b % a.m_ne3) * a.m_nb3)
-                         : (const uint16_t*)g_fa_zero_mask;
+        moff[m] = a.mask ? (uint32_t)((int64_t)(iq0 + qq) * a.m_nb1 + (int64_t)(h % a.m_ne2) * a.m_nb2) + 8u * lg : 0u;
     }
     // mask of a slice: lane (lr, lg) brings rows t + 4lg + 2k, +1 (k = 0, 1) of its
     // pair's mask row as one f16 pair into its slot of the wave's mask ring, in the
@@ -427,16 +423,35 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     // pair's limit and are replaced by -inf); the pair at the last row, when L is
     // odd, reads the aligned dword that holds it (the host requires 4-byte aligned
     // mask rows).
+    // The address is the sequence's mask plane (wave-uniform, in SGPRs; the
+    // slice's first row joins it) plus the lane's 32-bit offset moff[m] (its
+    // pair's row and head, then element 4lg; the host keeps a plane below 2^31
+    // bytes), so a full slice's mask loads take no vector instructions.
     const int mcols = a.mask ? (int)a.L : 0;
     uint8_t* mring = smem + C::MASKR + wave * C::MASK_W;
+    const uint8_t* mplane = a.mask ? a.mask + (int64_t)(b % a.m_ne3) * a.m_nb3 : (const uint8_t*)g_fa_zero_mask;
     auto load_mask = [&](int t, int st) {
+        if (!a.mask) {
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+            for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int r = t + 4 * lg + 2 * k;
-                lds_dma4_ptr(mrow[m] + (r < mcols ? r : 0), mring + (st * MT + m) * 512 + k * 256);
-            }
+                for (int k = 0; k < 2; ++k) lds_dma<4>(mplane, 0u, mring + (st * MT + m) * 512 + k * 256);
+        } else if (t + kSub <= mcols) {
+            const uint8_t* mt = mplane + 2 * (int64_t)t;
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) lds_dma<4>(mt, moff[m] + 4u * k, mring + (st * MT + m) * 512 + k * 256);
+        } else {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int r = t + 4 * lg + 2 * k;
+                    const uint32_t o = r < mcols ? moff[m] + (uint32_t)(2 * t + 4 * k) : moff[m] - 8u * lg;
+                    lds_dma<4>(mplane, o, mring + (st * MT + m) * 512 + k * 256);
+                }
+        }
     };
 
     const int step = kSub * NW;
@@ -1352,6 +1367,9 @@ hipError_t fa_mma_launch(FaArgs a, const FaLaunch& L, hipStream_t stream) {
     a.q_nb2 = (int64_t)L.q->nb[2];
     a.q_nb3 = (int64_t)L.q->nb[3];
     if (!fa_mma_mask_ok(a)) return hipErrorInvalidValue;
+    // the mask loads address a sequence's plane with 32-bit lane offsets
+    if (a.mask && (int64_t)(a.NQ - 1) * a.m_nb1 + (int64_t)(a.m_ne2 - 1) * a.m_nb2 + 2 * a.L + 4 >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;
     const uint32_t n_wg = (uint32_t)a.n_splits * a.n_qtiles * a.Hkv * a.B;
     launch("fa_dec", fn, dim3(n_wg), dim3(64 * waves), stream, a);
     hipError_t e = hipGetLastError();
