@@ -308,8 +308,10 @@ def copy_ceiling(torch, total_bytes, n_sets, steps, warmup, read_only):
     call over `n_sets` rotated buffers (beyond the Infinity Cache): a device
     copy of half the bytes (read + write) and an elementwise pass over them,
     timed from HIP-graph replays like the op; with read_only, also a
-    reduction that reads all the bytes once (timed eagerly: torch's reduction
-    clears memory inside a graph), the shape of a read-dominated call."""
+    reduction that reads all the bytes once, the shape of a read-dominated
+    call: row sums over 64 KiB rows, torch's fastest read-only pass over these
+    bytes among its reductions (a whole-tensor sum takes 40 % longer), timed
+    eagerly (torch's reductions may clear memory inside a graph)."""
     half = total_bytes // 2 // 16 * 16
     bufs = [(torch.empty(half, dtype=torch.uint8, device="cuda"), torch.empty(half, dtype=torch.uint8, device="cuda"))
             for _ in range(n_sets)]
@@ -329,16 +331,20 @@ def copy_ceiling(torch, total_bytes, n_sets, steps, warmup, read_only):
                       "call_us_dist": c_stats}
         log(f"copy ceiling ({name}): {c_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
     if read_only:
-        whole = [torch.cat([a, b]).view(torch.float32) for a, b in bufs]  # all the bytes, read once
+        row = 16384  # floats per summed row
+        n_rows = 2 * half // 4 // row
+        whole = [torch.cat([a, b]).view(torch.float32)[: n_rows * row].view(n_rows, row) for a, b in bufs]
         del bufs, fbufs
-        res = torch.empty((), dtype=torch.float32, device="cuda")
+        res = torch.empty(n_rows, dtype=torch.float32, device="cuda")
 
         def read_call(i):
-            torch.sum(whole[i], dim=0, out=res)
+            torch.sum(whole[i], dim=1, out=res)
 
         r_ms = time_calls(torch, read_call, n_sets, steps, warmup)
-        ceil["read_sum"] = {"us_per_call": round(r_ms * 1000, 3), "GB/s": round(2 * half / (r_ms * 1e-3) / 1e9, 1)}
-        log(f"read ceiling (sum): {r_ms * 1000:.2f} us/call for {2 * half / 1e6:.1f} MB")
+        rb = n_rows * row * 4
+        ceil["read_rowsum"] = {"us_per_call": round(r_ms * 1000, 3), "GB/s": round(rb / (r_ms * 1e-3) / 1e9, 1),
+                               "bytes": rb}
+        log(f"read ceiling (row sums): {r_ms * 1000:.2f} us/call for {rb / 1e6:.1f} MB")
         del whole
     return ceil
 
@@ -444,16 +450,19 @@ def kernel_times(torch, xq, fn, n_sets, steps):
     return {k: {"avg_us": 1000.0 * ms / max(n, 1), "launches": n} for k, (ms, n) in res.items()}
 
 
-def cpu_fa_baseline(torch, wl, cfg, fa_set, threads, budget_s):
-    """ggml-CPU restatement on the same bytes (copied back to host)."""
+def cpu_fa_baseline(torch, wl, cfg, fa_set, threads, budget_s, min_runs=3, warm=True):
+    """ggml-CPU restatement on the same bytes (copied back to host): the median
+    of at least min_runs timed runs (up to 20, or until budget_s has passed),
+    after one untimed run when warm."""
     import numpy as np
     import oracle
     q, k, v, m, d = fa_set
     host = lambda dt, t: wl.HostTensor(dt.type, dt.ne, dt.nb, t.t.reshape(-1).view(torch.uint8).cpu().numpy())
     hq, hk, hv, hm = host(q, q), host(k, k), host(v, v), host(m, m)
     hd = wl.HostTensor(wl.F32, d.ne, d.nb, np.zeros(d.t.numel() * 4, np.uint8))
-    oracle.flash_attn_ext(hq, hk, hv, hm, None, hd, cfg.kq_scale, 0.0, 0.0, oracle.QK_CONSISTENT, True,
-                          threads, want_lse=False)  # warm-up
+    if warm:
+        oracle.flash_attn_ext(hq, hk, hv, hm, None, hd, cfg.kq_scale, 0.0, 0.0, oracle.QK_CONSISTENT, True,
+                              threads, want_lse=False)
     times = []
     t_end = time.perf_counter() + budget_s
     while True:
@@ -461,7 +470,7 @@ def cpu_fa_baseline(torch, wl, cfg, fa_set, threads, budget_s):
         oracle.flash_attn_ext(hq, hk, hv, hm, None, hd, cfg.kq_scale, 0.0, 0.0, oracle.QK_CONSISTENT, True,
                               threads, want_lse=False)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 3 and time.perf_counter() > t_end:
+        if len(times) >= min_runs and time.perf_counter() > t_end:
             break
         if len(times) >= 20:
             break
@@ -626,6 +635,7 @@ def main():
             out["copy_ceiling"] = copy_ceiling(torch, alg, n_sets, args.steps, args.warmup, read_only=True)
 
     # ---------------- the other attention configs: f16 decode at 4k, q4_0 MTP verify
+    x_first = {}  # key -> (config, its first input set, its call), for the CPU baselines
     if args.only in ("fa", "all"):
         for key, xcfg, comp in (("fa_decode_f16", wl.FA_C1, "f16 MFMA scores (f32 Q as f16 hi + lo) and values "
                                                              "(weights as f16 hi + lo), f32 accumulation"),
@@ -661,7 +671,8 @@ def main():
                         "kernel_us_dist": {k: dist_ms(v) for k, v in xks.items()},
                         "input_sets": x_sets_n, "timed_calls": x_n, "kernels": xkt}
             log(f"{key}: {x_ms * 1000:.2f} us/call, fa_dec {x_kus:.2f} us")
-            del xsets, xws
+            x_first[key] = (xcfg, xsets[0], lambda x_call=x_call: x_call(0))
+            del xsets
 
     # ---------------- GDN decode step
     gcfg = wl.GDN_C3
@@ -778,6 +789,20 @@ def main():
                 "one_thread": {"value": round(alg / t1 / 1e9, 3), "us_per_call": round(t1 * 1e6, 1),
                                "median_of": n1},
                 "host": host, "gpu_vs_cpu_max_abs_err": max_err}
+            # C1 and C5: the same loop on their full calls; C5's one-thread leg takes
+            # one timed run (about 7 s) after the multi-thread runs have warmed it
+            for key, (xcfg, xset, xrun) in x_first.items():
+                xrun()
+                torch.cuda.synchronize()
+                log(f"CPU baseline: {key} on {threads} threads and on 1")
+                t_x, n_x, x_err = cpu_fa_baseline(torch, wl, xcfg, xset, threads, args.cpu_budget / 4)
+                t_x1, n_x1, _ = cpu_fa_baseline(torch, wl, xcfg, xset, 1, args.cpu_budget / 4,
+                                                min_runs=1, warm=False)
+                x_alg = xcfg.algorithmic_bytes()
+                out[key]["cpu_baseline"] = {"us_per_call": round(t_x * 1e6, 1), "cores": threads, "kind": "port",
+                                            "GB/s": round(x_alg / t_x / 1e9, 3), "median_of": n_x,
+                                            "one_thread_us_per_call": round(t_x1 * 1e6, 1),
+                                            "one_thread_median_of": n_x1, "gpu_vs_cpu_max_abs_err": x_err}
         if args.only in ("gdn", "all"):
             gdn_call(0)
             torch.cuda.synchronize()
