@@ -542,7 +542,7 @@ def main():
         print(json.dumps(rec))
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+        print(json.dumps({"error": "this bench runs on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
@@ -789,8 +789,9 @@ def main():
                 "one_thread": {"value": round(alg / t1 / 1e9, 3), "us_per_call": round(t1 * 1e6, 1),
                                "median_of": n1},
                 "host": host, "gpu_vs_cpu_max_abs_err": max_err}
-            # C1 and C5: the same loop on their full calls; C5's one-thread leg takes
-            # one timed run (about 7 s) after the multi-thread runs have warmed it
+            # the 4k f16 decode and the q4_0 verify: the same loop on their full calls;
+            # the verify's one-thread leg takes one timed run (about 5 s) after the
+            # multi-thread runs have warmed it
             for key, (xcfg, xset, xrun) in x_first.items():
                 xrun()
                 torch.cuda.synchronize()

@@ -4,7 +4,8 @@
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
  * ggml CPU semantics (the ggml sources themselves are not available to build).
  * Only the test suite, the smoke check and the benchmark's CPU-baseline leg may
- * load it, and only as the checker; the product library never links it.
+ * load it, and only as the reference results are compared with; the product
+ * library never links it.
  *
  * Each function cites the reference file:line it restates. Functions marked
  * "parity unpinned at bit level" follow upstream ggml's published algorithm

@@ -61,7 +61,7 @@ def _selftest_inputs(T, B, seed=1701):
     return q, k, v, g, beta, st
 
 
-def make_gdn_case(T, slots, B=1, dist="north_star", seed=1234, pad=0, bf16=False, v_scale=1.0,
+def make_gdn_case(T, slots, B=1, dist="model", seed=1234, pad=0, bf16=False, v_scale=1.0,
                   qk_edit=None) -> GdnCase:
     """v_scale multiplies v and the initial state (the recurrence is linear in
     them); qk_edit(q, k) edits the f32 q [B,T,16,128] and k rows in place

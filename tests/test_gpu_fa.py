@@ -1,7 +1,7 @@
 """GPU parity of GGML_OP_FLASH_ATTN_EXT (gfx950 kernels through the C ABI) against
 the ggml-CPU restatement in oracle/, at the benchmark configurations' full sizes.
 
-Tolerance (north star): max-abs 2e-3 / rel 1e-2 elementwise, f32 accumulation
+Tolerance (the ops' parity bar): max-abs 2e-3 / rel 1e-2 elementwise, f32 accumulation
 on the GPU; ggml's CPU path accumulates F16 V in an f16 vector, so the F16
 config is also compared with the float64 closed form as the tie-break.
 """

@@ -1,6 +1,6 @@
 """GPU numerics of GGML_OP_FLASH_ATTN_EXT beyond the N(0,1) configurations:
 
-* the value path's accuracy does not depend on V's magnitude (C2 / C5 geometry,
+* the value path's accuracy does not depend on V's magnitude (the 32k q8_0 decode's and the q4_0 verify's geometry,
   V scaled by 1e-1 .. 1e-3, both engines, 1e-5 relative to max|f64|);
 * KV dequantisation inside the kernels is bit-exact: with Q = 0 and one visible
   row per (query, head) the output is that row's dequantised V, bit for bit
@@ -310,7 +310,7 @@ def test_fa_query_width_invariance_c2_geometry(torch_gpu, kv_type, engine):
     """n_q = 1, 3 and 8 give the same bits for a query at L = 32768, D = 256,
     GQA 6, B = 4 (2048-row splits: many 16-row slices per wave)."""
     cfg = wl.FaConfig("inv_c2", 8, 24, 4, 256, 32768, 4, kv_type, causal_prefix=32760)
-    case_note(f"query width invariance C2 geometry {wl.TYPE_NAME[kv_type]} engine {engine}")
+    case_note(f"query width invariance 32k q8_0 decode geometry {wl.TYPE_NAME[kv_type]} engine {engine}")
     case = _cached_case(cfg, seed=5)
     batch, blse = run_fa_gpu(case, torch_gpu, engine=engine)
     for iq0, n in ((0, 1), (3, 1), (7, 1), (2, 3), (5, 3)):
@@ -374,18 +374,18 @@ def test_fa_sequence_batch_invariance_length_only_split_modes(torch_gpu, engine,
 
 @pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
 def test_fa_verify_full_size_masked_query_rows(torch_gpu, engine):
-    """C5 at full size (n_q 8, L 16392, q4_0, B 8) with the mask padded to 16
+    """The q4_0 verify at full size (n_q 8, L 16392, B 8) with the mask padded to 16
     rows and queries 6 and 7 fully masked (-inf rows): those give O = 0 and
     LSE = -inf, the others match the oracle."""
     cfg = dataclasses.replace(wl.FA_C5, name="c5_masked_rows", n_q_pad=16)
-    case_note(f"C5 full size masked query rows engine {engine}")
+    case_note(f"q4_0 verify full size masked query rows engine {engine}")
     case = make_fa_case(cfg, seed=12)
     m = wl.fa_causal_mask(cfg, n_q_rows=6)  # rows 6..15 all -inf
     case.mask = wl.mask_tensor(m)
     got, glse = run_fa_gpu(case, torch_gpu, engine=engine)
     assert np.all(got[:, 6:] == 0.0) and np.all(np.isneginf(glse[:, 6:]))
     want, wlse = oracle_fa(case)
-    assert_close(got, want, what="C5 masked query rows vs ggml restatement")
+    assert_close(got, want, what="q4_0 verify masked query rows vs ggml restatement")
     ref64, lse64 = oracle_f64(case)
-    assert_close(got[:, :6], ref64[:, :6], atol=1e-4, rtol=1e-4, what="C5 vs f64")
-    assert_close(glse[:, :6], lse64[:, :6], atol=1e-4, rtol=1e-5, what="C5 LSE")
+    assert_close(got[:, :6], ref64[:, :6], atol=1e-4, rtol=1e-4, what="q4_0 verify vs f64")
+    assert_close(glse[:, :6], lse64[:, :6], atol=1e-4, rtol=1e-5, what="q4_0 verify LSE")

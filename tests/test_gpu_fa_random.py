@@ -8,7 +8,7 @@ The shapes between the benchmark configurations are where the kernels' tile
 and split boundaries fall differently (ragged last slices, splits shorter than
 a slice, query tiles with idle pairs, GQA groups that do not divide 16).
 
-Tolerance (north star): max-abs 2e-3 / rel 1e-2 elementwise against the
+Tolerance (the ops' parity bar): max-abs 2e-3 / rel 1e-2 elementwise against the
 restatement and against float64. Relative to the largest output, the outputs
 stay within 1e-5 of float64 for every KV type: the value products keep about
 22 significant bits (f16 hi + lo operands) and accumulate in f32, so even short

@@ -7,7 +7,7 @@ Covers the full prefill (4096 bf16 tokens), partial last chunks, snapshot slots
 (the last slots - 1 tokens run on the step kernel from the chunked part's
 state), f32 and bf16 inputs, padded q/k/v rows and several sequences.
 
-Tolerance (north star): outputs and states within max-abs 2e-3 / rel 1e-2.
+Tolerance (the ops' parity bar): outputs and states within max-abs 2e-3 / rel 1e-2.
 """
 import numpy as np
 import pytest
@@ -35,18 +35,18 @@ def _check(case, got, want, what):
 def test_gdn_chunked_prefill_4096_bf16(torch_gpu):
     cfg = wl.GDN_C4
     case_note(f"gated_delta_net chunked {cfg.name}")
-    case = make_gdn_case(cfg.T, cfg.slots, B=cfg.B, dist="north_star", bf16=cfg.bf16, seed=77)
+    case = make_gdn_case(cfg.T, cfg.slots, B=cfg.B, dist="model", bf16=cfg.bf16, seed=77)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
-    err = _check(case, got, case.oracle(), "C4 chunked vs restated recurrence")
-    err64 = _check(case, got, case.oracle_f64(), "C4 chunked vs float64")
-    print(f"C4: max|gpu-oracle|={err:.2e} max|gpu-f64|={err64:.2e}")
+    err = _check(case, got, case.oracle(), "4096-token prefill vs restated recurrence")
+    err64 = _check(case, got, case.oracle_f64(), "4096-token prefill vs float64")
+    print(f"4096-token prefill: max|gpu-oracle|={err:.2e} max|gpu-f64|={err64:.2e}")
 
 
 def test_gdn_chunked_prefill_8_sequences(torch_gpu):
     """8 bf16 sequences of 1089 tokens at once (2048 scan workgroups, several per
     CU, and a one-token last chunk) against the restated recurrence."""
     case_note("gated_delta_net chunked T=1089 B=8 bf16")
-    case = make_gdn_case(1089, 1, B=8, dist="north_star", bf16=True, seed=78)
+    case = make_gdn_case(1089, 1, B=8, dist="model", bf16=True, seed=78)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     err = _check(case, got, case.oracle(), "chunked x8 vs restated recurrence")
     print(f"T=1089 B=8: max|gpu-oracle|={err:.2e}")
@@ -57,7 +57,7 @@ def test_gdn_chunked_prefill_8_sequences(torch_gpu):
                                        (200, 17, 1), (257, 5, 2), (64, 1, 1), (7, 2, 1)])
 def test_gdn_chunked_shapes(torch_gpu, T, slots, B, bf16):
     case_note(f"gdn chunked T={T} slots={slots} B={B} bf16={bf16}")
-    case = make_gdn_case(T, slots, B=B, dist="north_star", bf16=bf16, seed=T + 31 * slots)
+    case = make_gdn_case(T, slots, B=B, dist="model", bf16=bf16, seed=T + 31 * slots)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     err = _check(case, got, case.oracle_f64(), f"chunked T={T} K={slots} B={B}")
     print(f"T={T} K={slots} B={B} bf16={bf16}: max|gpu-f64|={err:.2e}")
@@ -75,7 +75,7 @@ def test_gdn_chunked_selftest_inputs(torch_gpu, T, slots):
 
 @pytest.mark.parametrize("pad", [3, 8])
 def test_gdn_chunked_padded_rows(torch_gpu, pad):
-    case = make_gdn_case(150, 2, B=2, dist="north_star", pad=pad, seed=3)
+    case = make_gdn_case(150, 2, B=2, dist="model", pad=pad, seed=3)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     _check(case, got, case.oracle_f64(), f"chunked padded rows pad={pad}")
 
@@ -83,7 +83,7 @@ def test_gdn_chunked_padded_rows(torch_gpu, pad):
 def test_gdn_chunked_matches_step_kernel(torch_gpu):
     """Both kernels compute the same recurrence; AUTO picks the chunked one
     for prefills longer than one chunk."""
-    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=True, seed=12)
+    case = make_gdn_case(300, 1, B=2, dist="model", bf16=True, seed=12)
     a = run_gpu(case, torch_gpu, mode=xqattn.GDN_STEP)
     b = run_gpu(case, torch_gpu, mode=xqattn.GDN_AUTO)
     c = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
@@ -98,7 +98,7 @@ def test_gdn_chunked_meets_reference_selftest_bar(torch_gpu, bf16):
     the float64 recurrence, at 300 tokens (4 full chunks + tail). f32 rows
     enter the matrix products as f16 hi + lo, bf16 rows exactly."""
     case_note(f"gdn chunked selftest bar bf16={bf16}")
-    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=bf16, seed=99)
+    case = make_gdn_case(300, 1, B=2, dist="model", bf16=bf16, seed=99)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     want = case.oracle_f64()
     v = _valid_rows(case)
@@ -110,7 +110,7 @@ def test_gdn_chunked_meets_reference_selftest_bar(torch_gpu, bf16):
 def test_gdn_chunked_strong_decay(torch_gpu):
     """Decays that underflow within a chunk (g = -40 per token) keep every
     factor in [0, 1] and the result finite."""
-    case = make_gdn_case(192, 1, B=1, dist="north_star", seed=21)
+    case = make_gdn_case(192, 1, B=1, dist="model", seed=21)
     g = np.frombuffer(case.g.buf.tobytes(), np.float32).copy()
     g[::3] = -40.0
     case.g.buf[:] = g.view(np.uint8)
@@ -143,7 +143,7 @@ def test_gdn_chunked_out_of_range_qk_runs_the_sequential_recurrence(torch_gpu, e
     and NaN exactly where the restated recurrence has it for a NaN k element
     (every later token and the final state of the two v-heads on that k-head)."""
     case_note(f"gdn chunked out-of-range {edit.__name__} bf16={bf16} pad={pad}")
-    case = make_gdn_case(300, 1, B=2, dist="north_star", bf16=bf16, seed=5, pad=pad, qk_edit=edit)
+    case = make_gdn_case(300, 1, B=2, dist="model", bf16=bf16, seed=5, pad=pad, qk_edit=edit)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     v = _valid_rows(case)
     if edit is _k_nan:
@@ -175,7 +175,7 @@ def test_gdn_chunked_magnitude_sweep(torch_gpu, v_scale, bf16):
     in range, so the reference selftest's bar max|gpu - want| / max|want| <= 1e-4
     holds against the float64 recurrence at every scale."""
     case_note(f"gdn chunked magnitude v_scale={v_scale} bf16={bf16}")
-    case = make_gdn_case(200, 1, B=1, dist="north_star", bf16=bf16, seed=41, v_scale=v_scale)
+    case = make_gdn_case(200, 1, B=1, dist="model", bf16=bf16, seed=41, v_scale=v_scale)
     got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
     want = case.oracle_f64()
     v = _valid_rows(case)
@@ -192,7 +192,7 @@ def test_gdn_graph_replays_match_eager(torch_gpu, mode, T):
     the output cleared before each replay and eager calls between the replays."""
     torch = torch_gpu
     case_note(f"gdn graph replays mode {mode} T {T}")
-    case = make_gdn_case(T, 3, B=2, dist="north_star", seed=23, bf16=True)
+    case = make_gdn_case(T, 3, B=2, dist="model", seed=23, bf16=True)
     dev = {n: xqattn.DevTensor.from_host(getattr(case, n)) for n in ("q", "k", "v", "g", "beta", "state")}
     dst = xqattn.DevTensor.from_host(case.dst)
     n_ws = xqattn.gated_delta_net_workspace(dev["q"], dev["v"], case.slots, mode)

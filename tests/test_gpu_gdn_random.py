@@ -4,7 +4,7 @@ sequences, row padding, f32 or bf16 q/k/v, and the step / chunked / AUTO
 modes, each case against the float64 recurrence (outputs, every kept snapshot
 and the untouched slots).
 
-Tolerance (north star): max-abs 2e-3 / rel 1e-2 elementwise, and the reference
+Tolerance (the ops' parity bar): max-abs 2e-3 / rel 1e-2 elementwise, and the reference
 selftest's max|gpu - want| / max|want| <= 1e-4 (src/bridge/ggml_d3d12.cpp:285-301).
 """
 import numpy as np
@@ -37,7 +37,7 @@ def test_gdn_random_shapes(torch_gpu, i):
     T, slots, B, pad, bf16, mode = draw_case(i)
     note = f"gdn random case {i}: T {T} slots {slots} B {B} pad {pad} bf16 {bf16} mode {mode}"
     case_note(note)
-    case = make_gdn_case(T, slots, B=B, dist="north_star", seed=4000 + i, pad=pad, bf16=bf16)
+    case = make_gdn_case(T, slots, B=B, dist="model", seed=4000 + i, pad=pad, bf16=bf16)
     got = run_gpu(case, torch_gpu, mode=mode)
     want = case.oracle_f64()
     valid = T + 128 * min(T, slots)

@@ -46,7 +46,7 @@ def test_graph_fa_and_gdn_match_direct_calls(torch_gpu):
     q, k, v, m = (xqattn.DevTensor.from_host(t) for t in (fa.q, fa.k, fa.v, fa.mask))
     d_graph = xqattn.DevTensor.empty_like_host(fa.dst)
     d_direct = xqattn.DevTensor.empty_like_host(fa.dst)
-    gdn = make_gdn_case(1, 1, B=2, dist="north_star", seed=5)
+    gdn = make_gdn_case(1, 1, B=2, dist="model", seed=5)
     dev = _dev_gdn(gdn)
     g_graph = xqattn.DevTensor.from_host(gdn.dst)
     g_direct = xqattn.DevTensor.from_host(gdn.dst)
@@ -76,7 +76,7 @@ def test_graph_orders_dependent_nodes(torch_gpu):
     """Two one-token GDN nodes, the second reading its state from the first
     node's final-state rows, equal one two-token node."""
     case_note("ggml graph: chained gdn steps T=1 -> T=1 vs T=2")
-    two = make_gdn_case(2, 1, B=1, dist="north_star", seed=11)
+    two = make_gdn_case(2, 1, B=1, dist="model", seed=11)
     full = _dev_gdn(two)
     d_two = xqattn.DevTensor.from_host(two.dst)
 
@@ -112,7 +112,7 @@ def test_graph_orders_dependent_nodes(torch_gpu):
 
 def test_graph_skips_non_compute_and_rejects_unsupported_before_launch(torch_gpu):
     case_note("ggml graph: skipped and rejected nodes")
-    gdn = make_gdn_case(1, 1, B=1, dist="north_star", seed=17)
+    gdn = make_gdn_case(1, 1, B=1, dist="model", seed=17)
     dev = _dev_gdn(gdn)
     dst = xqattn.DevTensor.from_host(gdn.dst)
     sentinel = dst.to_host_bytes().copy()
@@ -135,7 +135,7 @@ def test_graph_workspace_grows_once(torch_gpu):
     """A chunked prefill node grows the backend's workspace to its need; a
     later graph that needs less runs in the same workspace."""
     case_note("ggml graph: chunked gdn T=130 then step")
-    pre = make_gdn_case(130, 1, B=1, dist="north_star", seed=23, bf16=True)
+    pre = make_gdn_case(130, 1, B=1, dist="model", seed=23, bf16=True)
     dev = _dev_gdn(pre)
     dst = xqattn.DevTensor.from_host(pre.dst)
     need = xqattn.gated_delta_net_workspace(dev["q"], dev["v"], 1)
@@ -145,7 +145,7 @@ def test_graph_workspace_grows_once(torch_gpu):
         _run(be, [_gdn_node(dev, dst, 1)], torch_gpu)
         assert be.workspace_bytes == need
         assert_close(out_array(pre, dst.to_host_bytes()), pre.oracle(), what="chunked node vs oracle")
-        step = make_gdn_case(1, 1, B=2, dist="north_star", seed=29)
+        step = make_gdn_case(1, 1, B=2, dist="model", seed=29)
         sdev = _dev_gdn(step)
         sdst = xqattn.DevTensor.from_host(step.dst)
         _run(be, [_gdn_node(sdev, sdst, 1)], torch_gpu)
@@ -188,8 +188,8 @@ def test_graph_gdn_min_tokens_two_leaves_single_token_nodes_to_the_cpu(torch_gpu
     single-token GDN node is outside the backend's contract: the graph fails
     before any launch; a two-token node runs."""
     case_note("ggml graph: gdn_min_tokens 2")
-    one = make_gdn_case(1, 1, B=1, dist="north_star", seed=43)
-    two = make_gdn_case(2, 1, B=1, dist="north_star", seed=44)
+    one = make_gdn_case(1, 1, B=1, dist="model", seed=43)
+    two = make_gdn_case(2, 1, B=1, dist="model", seed=44)
     d1, d2 = _dev_gdn(one), _dev_gdn(two)
     o1, o2 = xqattn.DevTensor.from_host(one.dst), xqattn.DevTensor.from_host(two.dst)
     sentinel = o1.to_host_bytes().copy()

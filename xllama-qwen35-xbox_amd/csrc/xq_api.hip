@@ -556,7 +556,7 @@ xq_status xq_gated_delta_net(const xq_tensor* q, const xq_tensor* k, const xq_te
     if (st != XQ_OK) return st;
     if (mode < XQ_GDN_AUTO || mode > XQ_GDN_CHUNKED) return fail(XQ_ERR_BAD_ARG, "bad mode");
     if (mode == XQ_GDN_CHUNKED && !xq::gdn_chunked_available())
-        return fail(XQ_ERR_UNSUPPORTED, "chunked mode not available in this build");
+        return fail(XQ_ERR_UNSUPPORTED, "chunked mode not available in this library");
     for (const xq_tensor* t : {q, k, v, g, beta, state, (const xq_tensor*)dst})
         if (!t->data) return fail(XQ_ERR_BAD_ARG, "null data pointer");
     if (!aligned(state->data, 16) || !aligned(dst->data, 16))
