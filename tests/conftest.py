@@ -20,7 +20,7 @@ import oracle  # noqa: E402
 import xqattn  # noqa: E402
 from xqattn import workloads as wl  # noqa: E402
 
-# north-star tolerance for attention outputs and GDN outputs/state (f32 accumulation)
+# parity tolerance for attention outputs and GDN outputs/state (f32 accumulation)
 ATOL, RTOL = 2e-3, 1e-2
 
 
@@ -53,7 +53,7 @@ def torch_gpu():
 
 
 def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
-    """|got - want| <= atol + rtol*|want| elementwise."""
+    """|got - want| <= atol + rtol*|want| elementwise (the parity tolerance)."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     assert got.shape == want.shape, (got.shape, want.shape)

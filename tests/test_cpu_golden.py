@@ -37,7 +37,7 @@ def test_fa_fixture_oracle_bit_exact(path):
                                          oracle.QK_CONSISTENT, True, 8)
     assert np.array_equal(out64.astype(np.float32), a["out64"])
     assert np.array_equal(lse64.astype(np.float32), a["lse64"])
-    # the stored ggml-loop result and the closed form agree to the north-star bar
+    # the stored ggml-loop result and the closed form agree to the parity tolerance
     assert_close(a["out"], a["out64"], what=f"{path.stem}: ggml loop vs float64")
 
 

@@ -4,7 +4,7 @@ graph order on the backend's stream, with the synchronous contract of the
 reference backend (src/bridge/ggml_d3d12.cpp:1836-1942, synchronize = nullptr).
 
 Each node's result must equal the direct C-ABI call on the same inputs bit for
-bit (same kernels, same policy), and the oracle within the north-star
+bit (same kernels, same policy), and the oracle within the parity
 tolerance (2e-3 abs / 1e-2 rel). A later node reads an earlier node's output
 (the GDN state carried through a view of the first node's snapshot rows), a
 node without the compute flag is skipped, and an unsupported node fails the

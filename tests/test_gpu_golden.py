@@ -2,7 +2,7 @@
 the expected outputs were written by the oracle when the fixtures were made,
 so these checks need nothing but the fixtures and the C ABI.
 
-Tolerances: attention and GDN outputs within the north-star 2e-3 abs / 1e-2 rel
+Tolerances: attention and GDN outputs within the parity tolerance 2e-3 abs / 1e-2 rel
 of the ggml-loop result and of the float64 closed form; LSE within 1e-4 abs +
 1e-5 rel of float64; range attention within the reference's GPU bar
 (3e-4 + 3e-4|ref| for O, 3e-4 + 3e-5|ref| for LSE); KV append bit-exact.

@@ -1,7 +1,7 @@
 """XFA1 capture replay on the GPU: a capture of each multi-query golden fixture
 (permuted Q, K/V as views into a larger cache with junk in the gap rows) run
 through xq_flash_attn_ext via xqattn.xfa1.replay, against the captured output
-(the oracle's ggml-loop result) and the float64 closed form, at the north-star
+(the oracle's ggml-loop result) and the float64 closed form, at the parity
 tolerance 2e-3 abs / 1e-2 rel.
 """
 import pytest

@@ -224,7 +224,7 @@ def fa_causal_mask(cfg: FaConfig, n_q_rows: int | None = None) -> np.ndarray:
 
 
 def gdn_inputs(cfg: GdnConfig, seed: int = 1234, state_scale: float = 0.1):
-    """North-star GDN distributions: q, k L2-normalised N(0,1) per (token, head);
+    """The model's GDN input distributions: q, k L2-normalised N(0,1) per (token, head);
     v ~ N(0,1); beta = sigmoid(N(0,1)); g = -softplus(N(0,1)); S0 ~ 0.1*N(0,1).
     Returns float32 arrays q, k [B,T,16,128], v [B,T,32,128], g, beta [B,T,32],
     state [B,32,128,128]."""
