@@ -62,10 +62,12 @@ def _selftest_inputs(T, B, seed=1701):
 
 
 def make_gdn_case(T, slots, B=1, dist="model", seed=1234, pad=0, bf16=False, v_scale=1.0,
-                  qk_edit=None) -> GdnCase:
+                  qk_edit=None, vs_edit=None, gb_edit=None) -> GdnCase:
     """v_scale multiplies v and the initial state (the recurrence is linear in
-    them); qk_edit(q, k) edits the f32 q [B,T,16,128] and k rows in place
-    before they are stored."""
+    them); qk_edit(q, k) edits the f32 q [B,T,16,128] and k rows, vs_edit(v,
+    st) the f32 v [B,T,32,128] and the initial state [B,32,128 (c),128 (i)],
+    gb_edit(g, beta) the decays and betas [B,T,32], in place before they are
+    stored."""
     if dist == "selftest":
         q, k, v, g, beta, st = _selftest_inputs(T, B)
     else:
@@ -75,6 +77,10 @@ def make_gdn_case(T, slots, B=1, dist="model", seed=1234, pad=0, bf16=False, v_s
         st = (st * np.float32(v_scale)).astype(np.float32)
     if qk_edit is not None:
         qk_edit(q, k)
+    if vs_edit is not None:
+        vs_edit(v, st)
+    if gb_edit is not None:
+        gb_edit(g, beta)
     typ = wl.BF16 if bf16 else wl.F32
     if bf16:
         q, k, v = (oracle.f32_to_bf16(a) for a in (q, k, v))

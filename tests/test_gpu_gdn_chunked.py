@@ -167,6 +167,71 @@ def test_gdn_chunked_out_of_range_qk_runs_the_sequential_recurrence(torch_gpu, e
     assert rel <= 1e-4, rel
 
 
+def _v_nan(v, st):
+    v[0, 150, 2, 7] = np.float32(np.nan)
+
+
+def _v_inf(v, st):
+    v[1, 70, 9, 100] = np.float32(np.inf)
+
+
+def _state_nan(v, st):
+    st[0, 20, 33, 5] = np.float32(np.nan)  # head 20, column 33, key dim 5
+
+
+def _state_inf(v, st):
+    st[1, 30, 3, 1] = np.float32(-np.inf)
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+@pytest.mark.parametrize("edit", [_v_nan, _v_inf, _state_nan, _state_inf],
+                         ids=["v_nan", "v_inf", "state_nan", "state_inf"])
+def test_gdn_chunked_nonfinite_v_or_state_runs_the_sequential_recurrence(torch_gpu, edit, bf16):
+    """An Inf or NaN in v or in the entering state reaches exactly the outputs
+    the token recurrence gives it (its column from its token on; with the state,
+    the whole column): in the chunk products a zero of T or of the causal P
+    times it would be NaN in earlier tokens of its chunk, so the column block
+    that holds it runs token by token. The finite outputs stay within the
+    parity tolerance of the restated recurrence, the non-finite ones match its
+    NaN / Inf pattern."""
+    case_note(f"gdn chunked non-finite {edit.__name__} bf16={bf16}")
+    case = make_gdn_case(300, 1, B=2, dist="model", bf16=bf16, seed=6, vs_edit=edit)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    want = case.oracle()
+    v = _valid_rows(case)
+    bad = ~np.isfinite(want[:, :v])
+    assert bad.any() and not bad.all()
+    if edit is _v_nan:  # column 2 * 128 + 7 of sequence 0 from token 150 on, not before
+        assert np.isnan(want[0, 150:300, 2 * 128 + 7]).all() and np.isfinite(want[0, :150]).all()
+    _check(case, got, want, f"{edit.__name__} vs restated recurrence")
+
+
+def _g_positive(g, beta):
+    g[0, 100, 4] = np.float32(0.5)
+
+
+def _g_nan(g, beta):
+    g[1, 200, 17] = np.float32(np.nan)
+
+
+def _beta_inf(g, beta):
+    beta[0, 10, 31] = np.float32(np.inf)
+
+
+@pytest.mark.parametrize("edit", [_g_positive, _g_nan, _beta_inf], ids=["g_positive", "g_nan", "beta_inf"])
+def test_gdn_chunked_decay_outside_0_1_runs_the_sequential_recurrence(torch_gpu, edit):
+    """A g that is not finite or above 0 (a decay e^g outside [0, 1]) or a beta
+    that is not finite sends its (sequence, v-head) through the token
+    recurrence: the result is the restated recurrence's, non-finite pattern
+    included, and a growing decay stays within the parity tolerance."""
+    case_note(f"gdn chunked {edit.__name__}")
+    case = make_gdn_case(300, 1, B=2, dist="model", bf16=True, seed=8, gb_edit=edit)
+    got = run_gpu(case, torch_gpu, mode=xqattn.GDN_CHUNKED)
+    _check(case, got, case.oracle(), f"{edit.__name__} vs restated recurrence")
+    if edit is _g_positive:
+        _check(case, got, case.oracle_f64(), "positive g vs float64")
+
+
 @pytest.mark.parametrize("bf16", [True, False])
 @pytest.mark.parametrize("v_scale", [1e-6, 1e-3, 1e3, 1e6])
 def test_gdn_chunked_magnitude_sweep(torch_gpu, v_scale, bf16):

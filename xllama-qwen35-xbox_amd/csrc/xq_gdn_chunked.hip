@@ -38,7 +38,9 @@
 //                   the decays and G) is loaded into registers a chunk ahead,
 //                   in four parts spread over the chunk's phases. K^T is formed
 //                   in the scan from the K rows it already holds (the waves
-//                   share them through LDS, transposed), which keeps 16 KB per
+//                   share them through LDS: written transposed, or for bf16
+//                   rows read as 16-byte words written as loaded and read
+//                   with gfx950's transposing LDS read), which keeps 16 KB per
 //                   chunk out of every workgroup's operand fetch. P is formed
 //                   by the prep for bf16 rows read as 16-byte words (10 KB per
 //                   chunk, off the scan's chain; its products and decays are
@@ -60,15 +62,18 @@
 // power of two 2^a per (sequence, v-head, column block), chosen from the largest
 // |v| of the column block over the prefill and the largest |S| entering it so
 // that they lie in [1, 2), and divides Y and the final state by 2^a (exact). V
-// and the state may so have any f32 magnitude: f16's range holds a state that
-// grows 2^15-fold beyond them. q and k rows enter as f16 (or hi + lo) and meet
-// in f16 planes (the P tiles): the prep records per chunk whether they lie in
-// the range those operands hold (qk_in_range: |k| < 16, |q| < 2^15, |q| |k| <
-// 256 per element, finite; L2-normalised rows lie far inside), and a
-// (sequence, v-head) with any chunk outside it runs the token-by-token f32
-// recurrence in the scan instead (the sequential form's results, NaN / Inf
-// included). Inside the range each f16 element keeps an absolute precision of
-// about 2^-25 (in the scan's bf16 form the q and k rows are exact).
+// and the state may so have any finite f32 magnitude: f16's range holds a state
+// that grows 2^15-fold beyond them. q and k rows enter as f16 (or hi + lo) and
+// meet in f16 planes (the P tiles): the prep records per chunk whether they
+// lie in the range those operands hold (qk_in_range: |k| < 16, |q| < 2^15,
+// |q| |k| < 256 per element, finite; L2-normalised rows lie far inside) and
+// whether every decay e^g lies in [0, 1] and beta is finite (g finite and at
+// most 0, as the model's g = -softplus(..) is), and a (sequence, v-head) with
+// any chunk outside it runs the token-by-token f32 recurrence in the scan
+// instead (the sequential form's results, NaN / Inf included). So does a
+// column block whose v or entering state holds an Inf or NaN. Inside the range
+// each f16 element keeps an absolute precision of about 2^-25 (in the scan's
+// bf16 form the q and k rows are exact).
 #include <type_traits>
 
 #include "xq_kernels.h"
@@ -235,6 +240,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     __shared__ __attribute__((aligned(16))) float sG[2][64], sBeta[2][64], sEG[2][64];
     __shared__ uint32_t sVmax[2][kColBlocks];  // bits of the largest |v| per column block
     __shared__ uint32_t sQKmax[2];              // bits of the chunk's largest |k|, |q|
+    __shared__ uint32_t sGBout[2];              // per v-head: some g not finite or above 0, or beta not finite
     // f32 rows: the f16 remainders of K
     constexpr int NKL = BF16 ? 8 : 64 * KP;
     __shared__ __attribute__((aligned(16))) _Float16 sKl[NKL];
@@ -312,10 +318,10 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             }
         }
         // largest |v| of the token's 32 columns 32qt.. (two column blocks) for
-        // each v-head; a NaN compares as the largest bits, so it reaches the
-        // scan's choice
+        // each v-head; Inf and NaN compare as the largest bits, so they reach
+        // the scan's choice (which runs such a column block token by token)
         if (tid < 2 * kColBlocks) sVmax[tid / kColBlocks][tid % kColBlocks] = 0;
-        if (tid < 2) sQKmax[tid] = 0;
+        if (tid < 2) sQKmax[tid] = 0, sGBout[tid] = 0;
         uint32_t vm[2][2] = {{0, 0}, {0, 0}};
         if (ok) {
 #pragma unroll
@@ -346,8 +352,14 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         if (tid < 128) {
             const int e2 = tid >> 6, tt = t0 + (tid & 63), h = kh + 16 * e2;
             const bool ok2 = tt < a.T;
-            sG[e2][tid & 63] = ok2 ? *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)tt * a.g_nb2 + (int64_t)h * a.g_nb1) : 0.0f;
-            sBeta[e2][tid & 63] = ok2 ? *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)tt * a.b_nb2 + (int64_t)h * a.b_nb1) : 0.0f;
+            const float gv = ok2 ? *(const float*)(a.g + (int64_t)b * a.g_nb3 + (int64_t)tt * a.g_nb2 + (int64_t)h * a.g_nb1) : 0.0f;
+            const float bv = ok2 ? *(const float*)(a.beta + (int64_t)b * a.b_nb3 + (int64_t)tt * a.b_nb2 + (int64_t)h * a.b_nb1) : 0.0f;
+            sG[e2][tid & 63] = gv;
+            sBeta[e2][tid & 63] = bv;
+            // the chunked form takes decays e^g in [0, 1]: g finite and <= 0
+            // (differences of cumulative log-decays stay finite and the
+            // factors e^{G_t - G_j} at most 1), beta finite
+            if (!(gv <= 0.0f && gv > -INFINITY && __builtin_isfinite(bv))) atomicOr(&sGBout[e2], 1u);
         }
     }
     __syncthreads();
@@ -517,7 +529,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
             dec[64 + tid] = __expf(GC - G);
             dec[kRecG + tid] = G;
             if (tid == 0) dec[128] = __expf(GC);
-            if (tid == 1) dec[kRecRange] = qk_in_range(sQKmax[0], sQKmax[1]) ? 0.0f : 1.0f;
+            if (tid == 1) dec[kRecRange] = qk_in_range(sQKmax[0], sQKmax[1]) && !sGBout[e2] ? 0.0f : 1.0f;
             if (tid < kColBlocks) dec[kRecVmax + tid] = __uint_as_float(sVmax[e2][tid]);
         }
         if constexpr (RAW) {  // P[t][j] = (q_t . k_j) e^{G_t - G_j} (j <= t), f16 hi + lo
@@ -621,6 +633,17 @@ XQ_DEV h8 decode8(const uint4 (&w)[KW], bool ok) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = ok ? (_Float16)x[e] : (_Float16)0.0f;
     return r;
+}
+
+// Four 16-bit elements read transposed from LDS (gfx950 ds_read_b64_tr_b16):
+// in each group of 16 lanes, lane 4j + q addresses 4 consecutive elements of
+// row j of a 4 x 16 block (columns 4q .. 4q + 3), and lane m of the group
+// receives column m of that block, rows 0..3, in order.
+XQ_DEV uint2 lds_read_tr16(const _Float16* p) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(__attribute__((address_space(3))) short*)p);
+    return __builtin_bit_cast(uint2, v);
 }
 
 // A buffer resource over one workspace record (raw: byte offsets, no stride;
@@ -803,10 +826,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sWm[RAW ? kCols * TP : 8];
     // K rows of the chunk [t][i] (f16 hi, and lo for f32 rows): the A operands of P^T = K Q^T
     __shared__ __attribute__((aligned(16))) _Float16 sKh[RAW ? 8 : 64 * SP], sKl[BF16 ? 8 : 64 * SP];
-    // K^T [i][t] of the chunk, by chunk parity (read after the step's last
-    // barrier, so the next chunk writes the other one): the A operands of the
-    // state update
-    constexpr int KTP = 72;  // K^T rows (halves)
+    // The state update's A operands K^T, by chunk parity (read after the step's
+    // last barrier, so the next chunk writes the other one): K^T [i][t] (f16
+    // hi, and lo for f32 rows), or in the bf16 operand form (RAW) the chunk's K
+    // rows [t][i] as loaded, pitch KRP, which the update reads transposed
+    // (lds_read_tr16). Both layouts take 128 x KTP = 64 x KRP halves.
+    constexpr int KTP = 72;   // K^T rows (halves)
+    constexpr int KRP = 144;  // RAW: K rows (halves; 288 bytes, rows 8 banks apart)
+    static_assert(128 * KTP == 64 * KRP, "one buffer for both layouts");
     __shared__ __attribute__((aligned(16))) _Float16 sKTh[2][128 * KTP], sKTl[2][BF16 ? 8 : 128 * KTP];
 
     const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
@@ -859,14 +886,19 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         if (lane == 0) sAm[wave] = am;
     }
     __syncthreads();
-    if (sOut[0] | sOut[1] | sOut[2] | sOut[3]) {  // workgroup-uniform
+    // an Inf or NaN among the column block's v or entering state: the chunked
+    // products would carry it into earlier tokens of its chunk (a zero of T
+    // times it is NaN), so the block runs token by token, as the recurrence
+    // spreads it
+    const uint32_t am_all = max(max(sAm[0], sAm[1]), max(sAm[2], sAm[3]));
+    if ((sOut[0] | sOut[1] | sOut[2] | sOut[3]) || am_all >= 0x7f800000u) {  // workgroup-uniform
         scan_sequential<BF16>(a, b, h, cb, wave, lane);
         return;
     }
     int pa = 0;  // the power a
     {
-        const float m = __uint_as_float(max(max(sAm[0], sAm[1]), max(sAm[2], sAm[3])));
-        if (m > 0.0f && __builtin_isfinite(m)) {
+        const float m = __uint_as_float(am_all);
+        if (m > 0.0f) {
             int ex;
             (void)frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
             pa = min(max(1 - ex, -100), 100);
@@ -894,11 +926,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
                 // enter meets a zero T row or column, so they add nothing
                 rk[ks] = C.kw[ks][0];
                 rq[ks] = C.qw[ks][0];
-                const uint32_t u[4] = {rk[ks].x, rk[ks].y, rk[ks].z, rk[ks].w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    ((uint16_t*)kth)[(32 * ks + 8 * lg + e) * KTP + 16 * wave + lr] =
-                        (uint16_t)(e & 1 ? u[e >> 1] >> 16 : u[e >> 1]);
+                *(uint4*)(kth + (16 * wave + lr) * KRP + 32 * ks + 8 * lg) = rk[ks];
                 continue;
             }
             ak[ks] = decode8<BF16, VEC>(C.kw[ks], C.ok);
@@ -1101,7 +1129,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
                 f4 acc = S[a2] * C.eGC, acc2 = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
-                    const uint4 kt = *(const uint4*)(kth + (16 * (2 * wave + a2) + lr) * KTP + 32 * ks + 8 * lg);
+                    // K^T[16 it + lr][32 ks + 8 lg + j], j = 0..7: the 4 x 16 blocks
+                    // at tokens 32 ks + 8 lg (+ 4), key dims 16 it ..
+                    const _Float16* kb = kth + (32 * ks + 8 * lg + (lr >> 2)) * KRP + 16 * (2 * wave + a2) + 4 * (lr & 3);
+                    const uint2 k0 = lds_read_tr16(kb), k1 = lds_read_tr16(kb + 4 * KRP);
+                    const uint4 kt = make_uint4(k0.x, k0.y, k1.x, k1.y);
                     acc = mfma_bf(kt, bw[ks][0], acc);
                     acc2 = mfma_bf(kt, bw[ks][1], acc2);
                     acc2 = mfma_bf(kt, bw[ks][2], acc2);
