@@ -274,7 +274,11 @@ enum xq_gdn_mode {
     XQ_GDN_CHUNKED = 2,  /* 64-token chunks in the UT form on the matrix cores (f32
                             operands split into f16 hi + lo, or three bf16 terms
                             against bf16 rows); q/k/v row strides of 2^25 bytes
-                            or more run the token-sequential kernel instead */
+                            or more run the token-sequential kernel instead, and
+                            q/k rows outside the chunk operands' range, decays
+                            e^g outside [0, 1], a non-finite beta, or an Inf/NaN
+                            in v or the state run the token recurrence for the
+                            heads or column blocks concerned */
 };
 
 /* Pure predicate mirroring d3d12_gdn_supported (src/bridge/ggml_d3d12.cpp:77-109),
