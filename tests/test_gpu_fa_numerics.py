@@ -119,6 +119,83 @@ def test_fa_dequant_bit_exact_one_visible_row(torch_gpu, kv_type, D, split_mode,
     assert np.all(np.abs(lse) < 1e-6)
 
 
+# scales and elements at the formats' edges: f16 +-65504, +-0, the smallest
+# and largest subnormals; int8 -128 and 127; q4_0 nibbles 0 and 15; E5M2's
+# largest finite, subnormals and -0 (each quantized row keeps one scale, as a
+# row's blocks of a real cache lie within f16's range of one another)
+_F16_EDGES = [0x7BFF, 0xFBFF, 0x0001, 0x8001, 0x8000, 0x0000, 0x0400, 0x03FF, 0x83FF, 0x3C00, 0xBC00, 0x7800]
+_E5M2_EDGES = [0x7B, 0xFB, 0x01, 0x81, 0x80, 0x00, 0x04, 0x03, 0x3C, 0xBC, 0x78, 0x7A]
+_SCALE_EDGES = [0x7BFF, 0xFBFF, 0x0001, 0x8000, 0x03FF, 0x0400]
+
+
+def _edge_record(kv_type, D, j):
+    """Record j of the edge set (bytes) and its values, decoded here with numpy
+    from the block layouts (f16 d then int8 qs[32]; f16 d then 16 bytes, element
+    i < 16 the low nibble of byte i, element i >= 16 the high nibble of byte i - 16,
+    value (nibble - 8) d; E5M2 = the high byte of an f16)."""
+    if kv_type == wl.F16:
+        bits = np.array([_F16_EDGES[(i + j) % len(_F16_EDGES)] for i in range(D)], np.uint16)
+        return bits.view(np.uint8), bits.view(np.float16).astype(np.float32)
+    if kv_type == wl.E5M2:
+        b = np.array([_E5M2_EDGES[(i + j) % len(_E5M2_EDGES)] for i in range(D)], np.uint8)
+        return b, (b.astype(np.uint16) << 8).view(np.float16).astype(np.float32)
+    d_bits = np.uint16(_SCALE_EDGES[j % len(_SCALE_EDGES)])
+    d = np.float32(np.array([d_bits], np.uint16).view(np.float16)[0])
+    raw, vals = [], []
+    for blk in range(D // 32):
+        if kv_type == wl.Q8_0:
+            qs = np.array([(-128 + 8 * i + blk + j) % 256 - 128 if i else -128 for i in range(32)], np.int16)
+            qs[31] = 127
+            raw.append(np.concatenate([np.array([d_bits], np.uint16).view(np.uint8), qs.astype(np.int8).view(np.uint8)]))
+            vals.append(qs.astype(np.float32) * d)
+        else:
+            lo = np.array([(i + blk + j) % 16 for i in range(16)], np.uint8)
+            hi = np.array([15 - (i + blk) % 16 for i in range(16)], np.uint8)
+            raw.append(np.concatenate([np.array([d_bits], np.uint16).view(np.uint8), lo | (hi << 4)]))
+            vals.append((np.concatenate([lo, hi]).astype(np.float32) - np.float32(8)) * d)
+    return np.concatenate(raw), np.concatenate(vals).astype(np.float32)
+
+
+def _edge_case(kv_type, D):
+    """The one-visible-row case with edge records in six rows of both KV heads,
+    each seen alone by a (query, head) pair of its own."""
+    case, want = _one_row_case(kv_type, D)
+    vraw = np.frombuffer(case.v.buf.tobytes(), np.uint8).reshape(1, 300, 2, -1).copy()
+    mraw = np.frombuffer(case.mask.buf.tobytes(), np.uint16).reshape(8, 4, 300).copy()  # [H, n_q, L]
+    seen = {int(r) for r in np.argwhere(mraw == 0)[:, 2]}  # rows the other pairs see
+    edge_rows = [r for r in (50, 123, 211, 260, 299, 1, 2, 3, 4, 5, 6, 8, 9) if r not in seen][:6]
+    for j, r in enumerate(edge_rows):
+        for hk in range(2):
+            rec, vals = _edge_record(kv_type, D, j + 3 * hk)
+            vraw[0, r, hk] = rec
+        # (query j % 4, head 2 + j // 4) on KV head 0 and (j % 4, 6 + j // 4)
+        # on KV head 1 see row r only: a pair of its own for every edge row
+        iq = j % 4
+        for hk, h in ((0, 2 + j // 4), (1, 6 + j // 4)):
+            mraw[h, iq, :] = 0xFC00
+            mraw[h, iq, r] = 0
+            want[0, iq, h] = _edge_record(kv_type, D, j + 3 * hk)[1]
+    case = dataclasses.replace(case, v=wl.kv_tensor(vraw, kv_type, D),
+                               mask=wl.HostTensor(wl.F16, case.mask.ne, case.mask.nb, mraw.reshape(-1).view(np.uint8)))
+    return case, want
+
+
+@pytest.mark.parametrize("engine", ENGINES, ids=ENGINE_IDS)
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("kv_type", [wl.F16, wl.Q8_0, wl.Q4_0, wl.E5M2], ids=lambda t: wl.TYPE_NAME[t])
+def test_fa_dequant_bit_exact_edge_records(torch_gpu, kv_type, D, engine):
+    """The one-visible-row output of V records that hold the formats' edge values
+    is those values, bit for bit (zeros of either sign), for every query whose
+    visible row is an edge record."""
+    case_note(f"edge records {wl.TYPE_NAME[kv_type]} D{D} engine {engine}")
+    case, want = _edge_case(kv_type, D)
+    got, lse = run_fa_gpu(case, torch_gpu, engine=engine)
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} elements differ, first {bad[0]}: {got[tuple(bad[0])]} vs {want[tuple(bad[0])]}"
+    nz = want != 0
+    assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # non-finite records
 # ---------------------------------------------------------------------------
