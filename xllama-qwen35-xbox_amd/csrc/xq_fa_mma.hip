@@ -1202,10 +1202,15 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
 
     // ---- merge the wave states per 16-pair group through LDS (fixed wave order)
     const int64_t rows_per_seq = (int64_t)a.NQ * a.H;
-    __syncthreads();  // every wave is done with its ring and the Q image
     // [NW][16][MS]: rows padded by 4 floats so the 16 rows a write instruction
-    // touches start on different banks (unpadded, a 16-way conflict)
+    // touches start on different banks (unpadded, a 16-way conflict). With one
+    // pair group whose 16 rows fit in a wave's own ring (OWN), each wave writes
+    // them there as soon as its rows are done, without waiting for the others:
+    // its ring is its own, and no other wave reads it.
     constexpr int MS = C::MS;
+    constexpr bool OWN = MT == 1 && 16 * MS * 4 <= C::RING_W;
+    constexpr int WST = OWN ? C::RING_W / 4 : 16 * MS;  // a wave's rows (floats)
+    if constexpr (!OWN) __syncthreads();  // every wave is done with its ring and the Q image
     float* mb = (float*)smem;
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -1216,7 +1221,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
             sM[wave][16 * m + lr] = m_run[m] == -INFINITY ? -INFINITY : m_run[m] + kPOff;
             sL[wave][16 * m + lr] = lt;
         }
-        float* mw = mb + (wave * 16 + lr) * MS;
+        float* mw = mb + wave * WST + lr * MS;
         // the lane's dims of block c as 16-byte writes (acc_dim's layout);
         // padding pairs are never read
         if (16 * m + lr < npa) {
@@ -1249,7 +1254,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 const float mw_ = sM[w][p];
                 const float ew = mw_ == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw_ - M);
                 Ls = fmaf(sL[w][p], ew, Ls);
-                o += ew * *(const f4*)(mb + (w * 16 + pl) * MS + 4 * d4);
+                o += ew * *(const f4*)(mb + w * WST + pl * MS + 4 * d4);
             }
             const int qq = p / a.G, h = g_kv * a.G + p % a.G, iq = iq0 + qq;
             const int64_t row = (int64_t)b * rows_per_seq + (int64_t)iq * a.H + h;
@@ -1279,7 +1284,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
                 if (d4 == 0) a.part_ml[row * a.n_splits + split] = make_float2(Mn, Ls);
             }
         }
-        __syncthreads();
+        if (m + 1 < MT) __syncthreads();  // the next group reuses the rows
     }
 }
 
