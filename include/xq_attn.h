@@ -95,7 +95,11 @@ enum xq_fa_qk_policy {
  * assignment) depends on the head dim and GQA group only, so a query's result
  * is bitwise independent of how many queries share the call
  * (patches/0008-flash-attn-query-consistency.patch:40-56). Partial states
- * are merged in ascending split order.
+ * are merged in ascending split order. A split is rows_per_split contiguous
+ * rows, except in the matrix-core engine under AUTO and LENGTH (no positions):
+ * there the splits take the KV rows in groups of 128 (8 waves x 16-row
+ * slices) in turn, split s the groups s, s + n, s + 2n, ... of n splits, so
+ * their sizes differ by at most one group whatever the KV length.
  *  XQ_FA_SPLIT_AUTO: MI355X policy, about 256 / (sequences x KV heads) splits
  *    (one workgroup per CU), rows a multiple of 16 and at least 256 per split
  *    (at most ceil(L/256) splits). It depends on the number
@@ -261,7 +265,9 @@ xq_status xq_fa_params_from_env(xq_fa_params* params);
 /* Split count the policy picks for a KV length (host-side, pure; AUTO is
  * evaluated for one sequence and one KV head). */
 int32_t xq_fa_split_count(int64_t kv_len, int32_t split_mode);
-/* Rows per split for that policy (the last split may be shorter). */
+/* Rows per split for that policy (the last split may be shorter; the
+ * interleaved AUTO / LENGTH splits of the matrix-core engine hold the same
+ * count of rows to within one 128-row group). */
 int64_t xq_fa_split_rows(int64_t kv_len, int32_t split_mode);
 
 /* ---------------------------------------------------------------------------

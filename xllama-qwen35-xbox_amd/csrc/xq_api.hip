@@ -155,6 +155,7 @@ struct FaPlan {
     int qk_mode, q_round_f16;
     int32_t n_splits;
     int64_t split_rows;
+    int interleave;  // this build's split modes (AUTO, LENGTH)
     size_t ws;
 };
 
@@ -222,6 +223,7 @@ xq_status fa_check(const xq_tensor* q, const xq_tensor* k, const xq_tensor* v,
     P.qk_mode = (k->type == XQ_TYPE_Q8_0 || k->type == XQ_TYPE_Q4_0) ? xq::kQkInt8 : xq::kQkFloat;
     P.q_round_f16 = (p->qk_policy == XQ_FA_QK_NATIVE && k->type == XQ_TYPE_F16) ? 1 : 0;
     split_policy(P.L, p->split_mode, B * Hkv, &P.n_splits, &P.split_rows);
+    P.interleave = p->split_mode == XQ_FA_SPLIT_AUTO || p->split_mode == XQ_FA_SPLIT_LENGTH;
     if (P.n_splits > 256) return fail(XQ_ERR_UNSUPPORTED, "more than 256 KV splits");
     const int npairs = P.G * xq::fa_query_tile(P.D, P.G, P.NQ);
     if (!xq::fa_kernel_available(P.kt, P.D, P.qk_mode, npairs))
@@ -334,6 +336,7 @@ xq_status xq_flash_attn_ext(const xq_tensor* q, const xq_tensor* k, const xq_ten
     L.q_round_f16 = P.q_round_f16;
     L.n_splits = P.n_splits;
     L.split_rows = P.split_rows;
+    L.interleave = P.interleave;
     L.poison = 0;
     L.engine = params->engine;
     L.positions = nullptr;

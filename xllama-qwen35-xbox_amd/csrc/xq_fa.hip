@@ -948,6 +948,7 @@ hipError_t fa_launch(const FaLaunch& L, hipStream_t stream) {
     a.lse = L.lse;
     a.L = k->ne[1];
     a.split_rows = L.split_rows > 0 ? L.split_rows : 1;
+    a.interleave = L.interleave && !L.positions && L.n_splits > 1 ? 1 : 0;
     a.H = H; a.Hkv = Hkv; a.G = G; a.NQ = NQ; a.B = B;
     a.rk3 = (int32_t)(B / k->ne[3]);
     a.rv3 = (int32_t)(B / v->ne[3]);

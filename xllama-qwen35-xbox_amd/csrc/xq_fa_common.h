@@ -46,6 +46,7 @@ struct FaArgs {
     float2* part_ml;
     int64_t L;
     int64_t split_rows;
+    int32_t interleave;  // fa_dec: split s takes the slice groups s, s + n_splits, ...
     int32_t H, Hkv, G, NQ, B, QT, n_qtiles, n_splits, rk3, rv3;
     float scale, softcap, max_bias, m0, m1;
     int32_t n_head_log2;

@@ -332,9 +332,12 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
     const int lg = lane >> 4;
 
     // ---- rows of this split (row indices are 32-bit: the host keeps L below
-    //      2^30); with positions each pair sees rows below its causal limit
-    const int r0 = split * (int)a.split_rows;
-    int r_end = (int)min(a.L, (int64_t)r0 + a.split_rows);
+    //      2^30): split_rows contiguous rows, or (interleave) every n_splits-th
+    //      group of NW 16-row slices (one per wave) from group `split` on, so
+    //      that the splits' row counts differ by at most one group whatever L
+    //      is. With positions each pair sees rows below its causal limit
+    const int r0 = a.interleave ? split * kSub * NW : split * (int)a.split_rows;
+    int r_end = a.interleave ? (int)a.L : (int)min(a.L, (int64_t)r0 + a.split_rows);
     int r_all = r_end;  // rows below every pair's limit (per-row limits apply past it)
     if (a.positions) {
         int lmax = 0, lmin = (int)a.L;
@@ -454,7 +457,7 @@ __global__ __launch_bounds__((64 * DecCfg<KT, D, MT>::NW)) void fa_dec(FaArgs a)
         }
     };
 
-    const int step = kSub * NW;
+    const int step = a.interleave ? kSub * NW * a.n_splits : kSub * NW;
     int t0 = r0 + kSub * wave;
     constexpr int VD = D / 64;
     constexpr int PPW = (NPP + NW - 1) / NW;

@@ -90,6 +90,9 @@ struct FaLaunch {
     int q_round_f16;         // float image rounded to f16 (NATIVE policy, F16 K)
     int n_splits;
     int64_t split_rows;
+    // matrix-core engine, no positions: the splits take the 16 x 8-row slice
+    // groups in turn instead of split_rows contiguous rows each
+    int interleave;
     int poison;              // reduce poisons non-finite partial states
     int engine;              // xq_fa_engine
     // range mode (positions != null): row r visible to query i iff
