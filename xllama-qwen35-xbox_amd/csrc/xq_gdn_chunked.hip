@@ -837,9 +837,11 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 sKTh[2][128 * KTP], sKTl[2][BF16 ? 8 : 128 * KTP];
 
     const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
-    const uint32_t wg = xcd_remap(blockIdx.x, n_wg);  // column blocks of a head adjacent (one XCD)
+    // column blocks of a head adjacent, then the two v-heads kh, kh + 16 that
+    // read the same K and Q rows: the 16 workgroups on one XCD (shared L2)
+    const uint32_t wg = xcd_remap(blockIdx.x, n_wg);
     const int cb = (int)(wg % kColBlocks);
-    const int h = (int)((wg / kColBlocks) % 32);
+    const int h = (int)((wg / (2 * kColBlocks)) % 16) + 16 * (int)((wg / kColBlocks) % 2);
     const int b = (int)(wg / (kColBlocks * 32));
     const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
 
