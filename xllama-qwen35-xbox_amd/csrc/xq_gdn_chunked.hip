@@ -252,8 +252,10 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
     _Float16* sQ = (_Float16*)sKK;  // RAW: Q [t][i] until the products are done
     static_assert(64 * FP * 4 >= 64 * KP * 2, "Q rows fit the L buffer");
 
-    // v-heads kh and kh + 16 share k-head kh: K K^T is formed once for both
-    const int n = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    // v-heads kh and kh + 16 share k-head kh: K K^T is formed once for both.
+    // The k-heads of a chunk are consecutive workgroups: they read the
+    // neighbouring parts of the same rows at about the same time.
+    const int n = blockIdx.y, kh = blockIdx.x, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int wave = wave_id(), lane = lane_id(), lr = lane & 15, lg = lane >> 4;
     const int t0 = n * kChunk;
@@ -1196,7 +1198,7 @@ bool gdn_chunked_available() { return true; }
 
 template <bool BF16, bool VEC>
 static void chunked_kernels(const GdnChunkArgs& a, hipStream_t stream) {
-    launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(a.n_chunks, 16, (uint32_t)a.B), dim3(256), stream, a);
+    launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(16, a.n_chunks, (uint32_t)a.B), dim3(256), stream, a);
     launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC>, dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), stream, a);
 }
 
