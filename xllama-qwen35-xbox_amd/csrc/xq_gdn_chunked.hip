@@ -88,7 +88,9 @@ constexpr int kChunk = 64;
 constexpr int kCols = 16;            // value columns per scan workgroup
 constexpr int kColBlocks = 128 / kCols;
 
-// Workspace record of one (sequence, v-head, chunk), byte offsets.
+// Workspace record of one (sequence, v-head, chunk), byte offsets. Records are
+// ordered (sequence, chunk, v-head): the prep's workgroups running at a time
+// write neighbouring records.
 constexpr int kRecTHi = 0;                       // f16 [64][64]
 constexpr int kRecTLo = kRecTHi + 64 * 64 * 2;
 constexpr int kRecDec = kRecTLo + 64 * 64 * 2;  // f32 e^G[64], e^{G_C - G}[64], e^{G_C}, range flag at 129, max|v|[8] at 136, G[64] at 192
@@ -507,7 +509,7 @@ __global__ __launch_bounds__(256, BF16 ? 2 : 1) void gdn_chunk_prep(GdnChunkArgs
         __syncthreads();
 
         // ---- the record: T (f16 hi + lo) with 16-byte stores, the decays and G
-        uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+        uint8_t* rec = a.ws + (((int64_t)b * a.n_chunks + n) * 32 + h) * kRecBytes;
         {
             const int t = tid >> 2, j0 = 16 * (tid & 3);
             h8 th[2], tl[2];
@@ -665,7 +667,7 @@ XQ_DEV void scan_load(const GdnChunkArgs& a, int b, int h, int cb, int n, int wa
     n = min(n, a.n_chunks - 1);  // the prefetch past the last chunk re-reads it
     const int row0 = n * kChunk;      // the chunk's first token
     const int last = a.T - 1 - row0;  // the chunk's rows past T read row T - 1 instead
-    const uint8_t* rec = a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes;
+    const uint8_t* rec = a.ws + (((int64_t)b * a.n_chunks + n) * 32 + h) * kRecBytes;
     // Row addresses are a wave-uniform base (sequence, head, chunk: scalar
     // registers) plus a 32-bit per-lane offset (the host keeps the row strides
     // below 2^25 bytes), so the loads take their base from SGPRs and the
@@ -875,7 +877,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) am = max(am, __float_as_uint(S[a2][r]) & 0x7fffffffu);
         for (int n = lane; n < a.n_chunks; n += 64) {
-            const float* dec = (const float*)(a.ws + (((int64_t)b * 32 + h) * a.n_chunks + n) * kRecBytes + kRecDec);
+            const float* dec = (const float*)(a.ws + (((int64_t)b * a.n_chunks + n) * 32 + h) * kRecBytes + kRecDec);
             am = max(am, __float_as_uint(dec[kRecVmax + cb]) & 0x7fffffffu);
             out_of_range |= dec[kRecRange] != 0.0f;
         }
