@@ -1102,7 +1102,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         if constexpr (RAW) {
             // through a buffer resource over the chunk's output rows: the
             // (head, column block) part of the offset in an SGPR, the lane's
-            // token and column in one VGPR
+            // token and column in one VGPR. Non-temporal: nothing here reads
+            // the outputs again
             const __amdgpu_buffer_rsrc_t r =
                 __builtin_amdgcn_make_buffer_rsrc((void*)(out + (int64_t)nn * kChunk * 4096), (short)0, 0x7fffffff, 0x00020000);
             const uint32_t so = 4u * (uint32_t)(h * 128 + kCols * cb);
@@ -1110,13 +1111,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
             for (int q = 0; q < 4; ++q) {
                 const int tl = 16 * wave + 4 * lg + q;  // token within the chunk
                 if (nn * kChunk + tl < a.T)
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[q] * yscale), r, (uint32_t)tl * 16384u + 4u * (uint32_t)lr, so, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[q] * yscale), r, (uint32_t)tl * 16384u + 4u * (uint32_t)lr, so, 2);
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int t = nn * kChunk + 16 * wave + 4 * lg + q;
-                if (t < a.T) out[(int64_t)t * 4096 + h * 128 + kCols * cb + lr] = y[q] * yscale;
+                if (t < a.T) __builtin_nontemporal_store(y[q] * yscale, out + (int64_t)t * 4096 + h * 128 + kCols * cb + lr);
             }
         }
 
