@@ -814,7 +814,9 @@ XQ_DEV void scan_sequential(const GdnChunkArgs& a, int b, int h, int cb, int wav
     for (int e = 0; e < 8; ++e) so[e] = s[e];
 }
 
-template <bool BF16, bool VEC>
+// NTY: the outputs Y are stored non-temporally (one workgroup per CU; see the
+// stores)
+template <bool BF16, bool VEC, bool NTY>
 __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
     constexpr int TP = 72;   // X^T, U^T rows [c][t] (halves)
     constexpr int SP = 136;  // S^T rows [c][i] (halves)
@@ -1102,22 +1104,32 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan(GdnChunkArgs a) {
         if constexpr (RAW) {
             // through a buffer resource over the chunk's output rows: the
             // (head, column block) part of the offset in an SGPR, the lane's
-            // token and column in one VGPR. Non-temporal: nothing here reads
-            // the outputs again
+            // token and column in one VGPR. Non-temporal when the scan runs one
+            // workgroup per CU (nothing here reads the outputs again, and the
+            // operands keep the L2); with two per CU (several sequences) the
+            // column blocks' partial lines merge better in L2
             const __amdgpu_buffer_rsrc_t r =
                 __builtin_amdgcn_make_buffer_rsrc((void*)(out + (int64_t)nn * kChunk * 4096), (short)0, 0x7fffffff, 0x00020000);
             const uint32_t so = 4u * (uint32_t)(h * 128 + kCols * cb);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int tl = 16 * wave + 4 * lg + q;  // token within the chunk
-                if (nn * kChunk + tl < a.T)
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, y[q] * yscale), r, (uint32_t)tl * 16384u + 4u * (uint32_t)lr, so, 2);
+                if (nn * kChunk + tl < a.T) {
+                    const uint32_t yv = __builtin_bit_cast(uint32_t, y[q] * yscale), vo = (uint32_t)tl * 16384u + 4u * (uint32_t)lr;
+                    __builtin_amdgcn_raw_buffer_store_b32(yv, r, vo, so, NTY ? 2 : 0);
+                }
             }
         } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int t = nn * kChunk + 16 * wave + 4 * lg + q;
-                if (t < a.T) __builtin_nontemporal_store(y[q] * yscale, out + (int64_t)t * 4096 + h * 128 + kCols * cb + lr);
+                if (t < a.T) {
+                    float* o = out + (int64_t)t * 4096 + h * 128 + kCols * cb + lr;
+                    if constexpr (NTY)
+                        __builtin_nontemporal_store(y[q] * yscale, o);
+                    else
+                        *o = y[q] * yscale;
+                }
             }
         }
 
@@ -1202,7 +1214,12 @@ bool gdn_chunked_available() { return true; }
 template <bool BF16, bool VEC>
 static void chunked_kernels(const GdnChunkArgs& a, hipStream_t stream) {
     launch("gdn_chunk_prep", gdn_chunk_prep<BF16, VEC>, dim3(16, a.n_chunks, (uint32_t)a.B), dim3(256), stream, a);
-    launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC>, dim3((uint32_t)a.B * 32 * kColBlocks), dim3(256), stream, a);
+    // one sequence: one scan workgroup per CU, non-temporal output stores
+    const uint32_t n_wg = (uint32_t)a.B * 32 * kColBlocks;
+    if (n_wg <= 256)
+        launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC, true>, dim3(n_wg), dim3(256), stream, a);
+    else
+        launch("gdn_chunk_scan", gdn_chunk_scan<BF16, VEC, false>, dim3(n_wg), dim3(256), stream, a);
 }
 
 hipError_t gdn_chunked_launch(const GdnLaunch& L, hipStream_t stream) {
