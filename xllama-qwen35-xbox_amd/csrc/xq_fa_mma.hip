@@ -7,8 +7,10 @@
 // on the 32k q8_0 decode, 21.4 against 28.8 us on the 4k f16 decode).
 //
 // Work decomposition. A workgroup owns one (sequence, KV head, query tile,
-// KV split). Its NW waves stream disjoint 16-row slices of the split (slice j
-// goes to wave j % NW) through private double-buffered LDS rings filled by
+// KV split). A split is a contiguous row range, or (AUTO and LENGTH split
+// modes) every n_splits-th group of NW slices. Its NW waves stream disjoint
+// 16-row slices of the split (slice j goes to wave j % NW) through private
+// double-buffered LDS rings filled by
 // global_load_lds, each with its own online softmax and no workgroup barrier
 // in the row loop. The wave states are merged through LDS at the end; with
 // several splits each workgroup writes a partial state (unnormalised output,
